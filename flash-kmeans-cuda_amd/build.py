@@ -1,0 +1,130 @@
+"""In-tree build of the gfx950 kernel library and its C++ consumers.
+
+Outputs (git-ignored, shipped with the tree to the GPU box):
+  flash_kmeans_cuda/libfkc.so                 C-ABI library (include/fkc.h)
+  flash_kmeans_cuda/libflash_kmeans_cuda.so   libtorch fkc:: API on top of it
+  flash_kmeans_cuda/bin/fkc_cpp_smoke         C++ smoke test of the fkc:: API
+
+Usage: python flash-kmeans-cuda_amd/build.py [--only capi|torch|all] [-j N]
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+PKG = os.path.join(HERE, "flash_kmeans_cuda")
+OBJ = os.path.join(HERE, "_build")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+# -packed-fp32-ops keeps the compiler from emitting v_pk_{add,mul,fma}_f32.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", INCLUDE, "-I", CSRC,
+]
+
+KERNEL_SOURCES = [
+    "assign_mfma.hip",
+    "assign_valu.hip",
+    "label_sort.hip",
+    "update.hip",
+    "finalize.hip",
+]
+HOST_SOURCES = ["capi.cpp"]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}):\n"
+                           f"{' '.join(cmd)}\n{proc.stdout}\n{err}")
+    if err.strip():
+        sys.stderr.write(err + "\n")
+
+
+def _compile(src: str) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    out = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+    path = os.path.join(CSRC, src)
+    lang = ["-x", "hip"] if src.endswith(".hip") else []
+    _run([HIPCC, *HIP_FLAGS, *lang, "-c", path, "-o", out])
+    return out
+
+
+def build_capi(jobs: int) -> str:
+    srcs = KERNEL_SOURCES + HOST_SOURCES
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(_compile, srcs))
+    lib = os.path.join(PKG, "libfkc.so")
+    tmp = lib + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs,
+          "-o", tmp])
+    os.replace(tmp, lib)
+    return lib
+
+
+def _torch_paths() -> tuple[list[str], str]:
+    import torch
+    root = os.path.dirname(torch.__file__)
+    incs = [os.path.join(root, "include"),
+            os.path.join(root, "include", "torch", "csrc", "api", "include")]
+    return incs, os.path.join(root, "lib")
+
+
+def build_torch_api() -> list[str]:
+    """libtorch fkc:: API (flash_kmeans_cuda.h) and its C++ smoke test."""
+    incs, tlib = _torch_paths()
+    api_dir = os.path.join(HERE, "torch_api")
+    cxx = shutil.which("g++") or "g++"
+    common = ["-O2", "-std=c++17", "-fPIC", "-D__HIP_PLATFORM_AMD__",
+              "-DUSE_ROCM", "-D_GLIBCXX_USE_CXX11_ABI=1",
+              "-I", INCLUDE, "-I", api_dir, "-I", os.path.join(ROCM, "include")]
+    for i in incs:
+        common += ["-isystem", i]
+    torch_libs = ["-L", tlib, "-Wl,-rpath," + tlib, "-ltorch", "-ltorch_cpu",
+                  "-ltorch_hip", "-lc10", "-lc10_hip", "-lamdhip64"]
+    lib = os.path.join(PKG, "libflash_kmeans_cuda.so")
+    _run([cxx, *common, "-shared", os.path.join(api_dir, "api.cpp"),
+          "-o", lib + ".tmp", "-L", PKG, "-Wl,-rpath,$ORIGIN", "-lfkc",
+          *torch_libs])
+    os.replace(lib + ".tmp", lib)
+    bindir = os.path.join(PKG, "bin")
+    os.makedirs(bindir, exist_ok=True)
+    exe = os.path.join(bindir, "fkc_cpp_smoke")
+    _run([cxx, *common, os.path.join(HERE, "cpp_tests", "smoke.cpp"),
+          "-o", exe + ".tmp", "-L", PKG, "-Wl,-rpath,$ORIGIN/..",
+          "-lflash_kmeans_cuda", "-lfkc", *torch_libs])
+    os.replace(exe + ".tmp", exe)
+    return [lib, exe]
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", choices=["capi", "torch", "all"], default="all")
+    ap.add_argument("-j", "--jobs", type=int,
+                    default=min(8, os.cpu_count() or 1))
+    args = ap.parse_args(argv)
+    if args.only in ("capi", "all"):
+        print(build_capi(args.jobs))
+    if args.only in ("torch", "all"):
+        for p in build_torch_api():
+            print(p)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

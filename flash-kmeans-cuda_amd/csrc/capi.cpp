@@ -1,0 +1,360 @@
+// extern "C" boundary: argument checks, workspace carving, the Lloyd loop.
+//
+// Validation mirrors what the reference checks before launching
+// (flash_kmeans_cuda/csrc/api.cpp:27-44, assign_sm80.cu:712-731,
+// update_sorted.cu:196-206, update_finalize.cu:76-83): shapes, dtypes and
+// non-null pointers.  Contiguity is the caller's contract (plain pointers).
+// Failures return a status and leave a message in fkc_last_error() instead of
+// throwing TORCH_CHECK errors across the ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "fkc_internal.hpp"
+
+namespace fkc {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(FKC_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return FKC_OK;
+}
+
+static bool env_true(const char* name) {
+  const char* s = std::getenv(name);
+  return s && (std::strcmp(s, "1") == 0 || std::strcmp(s, "true") == 0);
+}
+
+bool force_safe_assign() { return env_true("FKC_ASSIGN_FORCE_SAFE"); }
+
+int ntiles_override() {
+  const char* s = std::getenv("FKC_NTILES");
+  if (!s) return 0;
+  const int v = std::atoi(s);
+  return (v == 1 || v == 2 || v == 4) ? v : 0;
+}
+
+// ------------------------------------------------------------- profiling
+namespace {
+struct Profile {
+  bool enabled = false;
+  std::vector<hipEvent_t> starts, stops;
+  double total_ms = 0.0;
+  int64_t launches = 0;
+};
+Profile g_prof;
+
+void prof_clear_events() {
+  for (auto e : g_prof.starts) (void)hipEventDestroy(e);
+  for (auto e : g_prof.stops) (void)hipEventDestroy(e);
+  g_prof.starts.clear();
+  g_prof.stops.clear();
+}
+}  // namespace
+
+static int shape_ok(int64_t B, int64_t N, int64_t K, int64_t D,
+                    const char* what) {
+  if (B < 0 || N < 0 || K < 1 || D < 1)
+    return fail(FKC_ERR_INVALID, "%s: need B>=0, N>=0, K>=1, D>=1 (got %lld %lld %lld %lld)",
+                what, (long long)B, (long long)N, (long long)K, (long long)D);
+  if (B > 65535 || N > INT32_MAX - 65536 || K > INT32_MAX / 2 ||
+      D > (1 << 20))
+    return fail(FKC_ERR_UNSUPPORTED, "%s: shape out of supported range", what);
+  return FKC_OK;
+}
+
+static int dtype_ok(int dtype, const char* what) {
+  if (dtype != FKC_F32 && dtype != FKC_F16 && dtype != FKC_BF16)
+    return fail(FKC_ERR_INVALID, "%s: unsupported dtype %d", what, dtype);
+  return FKC_OK;
+}
+
+}  // namespace fkc
+
+// ------------------------------------------------------------- Lloyd loop
+namespace fkc {
+namespace {
+struct LoopBuffers {
+  float* x_sq = nullptr;   // only when the VALU assign route is taken
+  float* c_sq = nullptr;
+  int32_t* sorted = nullptr;
+  int32_t* perm = nullptr;
+  float* sums = nullptr;
+  int32_t* counts = nullptr;
+  float* shift = nullptr;  // one slot per iteration
+  int32_t* ctrl = nullptr; // [0] converged, [1] iterations run
+  void* sort_ws = nullptr;
+  size_t sort_ws_bytes = 0;
+  void* upd_ws = nullptr;
+  size_t upd_ws_bytes = 0;
+};
+
+LoopBuffers carve_loop(void* ws, int64_t B, int64_t N, int64_t K, int64_t D,
+                       int dtype, int max_iters, size_t* total) {
+  Carve c(ws);
+  LoopBuffers L;
+  if (!assign_uses_mfma(dtype, D)) L.x_sq = c.take<float>((size_t)B * N);
+  L.c_sq = c.take<float>((size_t)B * K);
+  L.sorted = c.take<int32_t>((size_t)B * N);
+  L.perm = c.take<int32_t>((size_t)B * N);
+  L.sums = c.take<float>((size_t)B * K * D);
+  L.counts = c.take<int32_t>((size_t)B * K);
+  L.shift = c.take<float>((size_t)(max_iters > 0 ? max_iters : 1));
+  L.ctrl = c.take<int32_t>(4);
+  L.sort_ws_bytes = sort_workspace_bytes(B, N, K);
+  L.sort_ws = c.take<char>(L.sort_ws_bytes);
+  L.upd_ws_bytes = update_workspace_bytes(B, N, D);
+  L.upd_ws = c.take<char>(L.upd_ws_bytes);
+  if (total) *total = c.used;
+  return L;
+}
+}  // namespace
+}  // namespace fkc
+
+using namespace fkc;
+
+extern "C" {
+
+const char* fkc_last_error(void) { return g_err; }
+const char* fkc_version(void) { return "0.1.0"; }
+
+int fkc_euclid_assign(const void* x, const void* centroids, const float* x_sq,
+                      const float* c_sq, int32_t* cluster_ids, int64_t B,
+                      int64_t N, int64_t K, int64_t D, int dtype,
+                      fkc_stream_t stream) {
+  g_err[0] = 0;
+  if (int rc = shape_ok(B, N, K, D, "euclid_assign")) return rc;
+  if (int rc = dtype_ok(dtype, "euclid_assign")) return rc;
+  if (B * N == 0) return FKC_OK;
+  if (!x || !centroids || !c_sq || !cluster_ids)
+    return fail(FKC_ERR_INVALID, "euclid_assign: null pointer argument");
+  return launch_assign(x, centroids, x_sq, c_sq, cluster_ids, B, N, K, D, dtype,
+                       nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fkc_row_sqnorm(const void* src, float* out, int64_t rows, int64_t D,
+                   int dtype, fkc_stream_t stream) {
+  g_err[0] = 0;
+  if (rows < 0 || D < 1)
+    return fail(FKC_ERR_INVALID, "row_sqnorm: need rows>=0, D>=1");
+  if (int rc = dtype_ok(dtype, "row_sqnorm")) return rc;
+  if (rows == 0) return FKC_OK;
+  if (!src || !out) return fail(FKC_ERR_INVALID, "row_sqnorm: null pointer");
+  return launch_row_sqnorm(src, out, rows, D, dtype, nullptr,
+                           reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t fkc_label_sort_workspace_bytes(int64_t B, int64_t N, int64_t K) {
+  if (B <= 0 || N <= 0 || K < 1) return 0;
+  return sort_workspace_bytes(B, N, K);
+}
+
+int fkc_label_sort(const int32_t* cluster_ids, int32_t* sorted_ids,
+                   int32_t* perm, int64_t B, int64_t N, int64_t K,
+                   void* workspace, size_t workspace_bytes,
+                   fkc_stream_t stream) {
+  g_err[0] = 0;
+  if (int rc = shape_ok(B, N, K, 1, "label_sort")) return rc;
+  if (B * N == 0) return FKC_OK;
+  if (!cluster_ids || !sorted_ids || !perm)
+    return fail(FKC_ERR_INVALID, "label_sort: null pointer argument");
+  return launch_label_sort(cluster_ids, sorted_ids, perm, B, N, K, false,
+                           workspace, workspace_bytes, nullptr,
+                           reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t fkc_update_workspace_bytes(int64_t B, int64_t N, int64_t D) {
+  if (B <= 0 || N <= 0 || D < 1) return 0;
+  return update_workspace_bytes(B, N, D);
+}
+
+static int update_common(const void* x, const int32_t* perm,
+                         const int32_t* ids_sorted, float* sums,
+                         int32_t* counts, int64_t B, int64_t N, int64_t K,
+                         int64_t D, int dtype, void* ws, size_t ws_bytes,
+                         fkc_stream_t stream, const char* what) {
+  g_err[0] = 0;
+  if (int rc = shape_ok(B, N, K, D, what)) return rc;
+  if (int rc = dtype_ok(dtype, what)) return rc;
+  if (B * N == 0) return FKC_OK;
+  if (!x || !ids_sorted || !sums || !counts)
+    return fail(FKC_ERR_INVALID, "%s: null pointer argument", what);
+  return launch_update(x, perm, ids_sorted, sums, counts, B, N, K, D, dtype,
+                       false, ws, ws_bytes, nullptr,
+                       reinterpret_cast<hipStream_t>(stream));
+}
+
+int fkc_centroid_update_sorted(const void* x_sorted, const int32_t* ids_sorted,
+                               float* sums, int32_t* counts, int64_t B,
+                               int64_t N, int64_t K, int64_t D, int dtype,
+                               void* workspace, size_t workspace_bytes,
+                               fkc_stream_t stream) {
+  return update_common(x_sorted, nullptr, ids_sorted, sums, counts, B, N, K, D,
+                       dtype, workspace, workspace_bytes, stream,
+                       "centroid_update_sorted");
+}
+
+int fkc_centroid_update_sorted_indexed(const void* x, const int32_t* sorted_idx,
+                                       const int32_t* ids_sorted, float* sums,
+                                       int32_t* counts, int64_t B, int64_t N,
+                                       int64_t K, int64_t D, int dtype,
+                                       void* workspace, size_t workspace_bytes,
+                                       fkc_stream_t stream) {
+  if (!sorted_idx && B * N > 0) {
+    g_err[0] = 0;
+    return fail(FKC_ERR_INVALID,
+                "centroid_update_sorted_indexed: null sorted_idx");
+  }
+  return update_common(x, sorted_idx, ids_sorted, sums, counts, B, N, K, D,
+                       dtype, workspace, workspace_bytes, stream,
+                       "centroid_update_sorted_indexed");
+}
+
+int fkc_centroid_finalize(const float* sums, const int32_t* counts,
+                          const void* old_centroids, void* out, int64_t B,
+                          int64_t K, int64_t D, int dtype,
+                          fkc_stream_t stream) {
+  g_err[0] = 0;
+  if (int rc = shape_ok(B, 0, K, D, "centroid_finalize")) return rc;
+  if (int rc = dtype_ok(dtype, "centroid_finalize")) return rc;
+  if (B == 0) return FKC_OK;
+  if (!sums || !counts || !old_centroids || !out)
+    return fail(FKC_ERR_INVALID, "centroid_finalize: null pointer argument");
+  return launch_finalize(sums, counts, old_centroids, out, nullptr, nullptr, B,
+                         K, D, dtype, nullptr,
+                         reinterpret_cast<hipStream_t>(stream));
+}
+
+
+size_t fkc_kmeans_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,
+                                  int dtype, int max_iters) {
+  if (B <= 0 || N <= 0 || K < 1 || D < 1) return 256;
+  size_t total = 0;
+  carve_loop(nullptr, B, N, K, D, dtype, max_iters, &total);
+  return total;
+}
+
+int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
+                     int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
+                     int max_iters, float tol, void* workspace,
+                     size_t workspace_bytes, fkc_stream_t stream,
+                     int32_t* n_iters_dev, int32_t* n_iters_host) {
+  g_err[0] = 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = shape_ok(B, N, K, D, "kmeans_lloyd")) return rc;
+  if (int rc = dtype_ok(dtype, "kmeans_lloyd")) return rc;
+  if (max_iters < 0) return fail(FKC_ERR_INVALID, "kmeans_lloyd: max_iters < 0");
+  if (B == 0 || N == 0 || max_iters == 0) {
+    if (n_iters_host) *n_iters_host = (B == 0 || N == 0) ? max_iters : 0;
+    if (n_iters_dev)
+      return launch_fill_i32(n_iters_dev, (B == 0 || N == 0) ? max_iters : 0,
+                             1, s);
+    return FKC_OK;
+  }
+  if (!x || !centroids || !cluster_ids)
+    return fail(FKC_ERR_INVALID, "kmeans_lloyd: null pointer argument");
+  size_t need = 0;
+  carve_loop(nullptr, B, N, K, D, dtype, max_iters, &need);
+  if (!workspace || workspace_bytes < need)
+    return fail(FKC_ERR_WORKSPACE, "kmeans_lloyd: workspace %zu < %zu bytes",
+                workspace_bytes, need);
+  LoopBuffers L = carve_loop(workspace, B, N, K, D, dtype, max_iters, nullptr);
+
+  const bool check = tol > 0.f;
+  const int32_t* ctrl = check ? L.ctrl : nullptr;
+  int rc = launch_fill_i32(L.ctrl, 0, 4, s);
+  if (!rc && check) rc = launch_fill_f32(L.shift, 0.f, max_iters, s);
+  if (!rc && L.x_sq) rc = launch_row_sqnorm(x, L.x_sq, B * N, D, dtype, nullptr, s);
+  if (!rc) rc = launch_row_sqnorm(centroids, L.c_sq, B * K, D, dtype, nullptr, s);
+  if (rc) return rc;
+
+  for (int it = 0; it < max_iters; ++it) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (g_prof.enabled) {
+      (void)hipEventCreate(&e0);
+      (void)hipEventCreate(&e1);
+      (void)hipEventRecord(e0, s);
+    }
+    rc = launch_assign(x, centroids, L.x_sq, L.c_sq, cluster_ids, B, N, K, D,
+                       dtype, ctrl, s);
+    if (g_prof.enabled) {
+      (void)hipEventRecord(e1, s);
+      g_prof.starts.push_back(e0);
+      g_prof.stops.push_back(e1);
+    }
+    if (!rc)
+      rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
+                             L.sort_ws, L.sort_ws_bytes, ctrl, s);
+    if (!rc)
+      rc = launch_update(x, L.perm, L.sorted, L.sums, L.counts, B, N, K, D,
+                         dtype, true, L.upd_ws, L.upd_ws_bytes, ctrl, s);
+    if (!rc)
+      rc = launch_finalize(L.sums, L.counts, centroids, centroids, L.c_sq,
+                           check ? L.shift + it : nullptr, B, K, D, dtype, ctrl,
+                           s);
+    if (!rc && check) rc = launch_converge_check(L.shift, it, tol, L.ctrl, s);
+    if (rc) return rc;
+  }
+  if (!check && n_iters_dev) rc = launch_fill_i32(n_iters_dev, max_iters, 1, s);
+  if (check && n_iters_dev) {
+    if (hipMemcpyAsync(n_iters_dev, L.ctrl + 1, sizeof(int32_t),
+                       hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: copy of iteration count failed");
+  }
+  if (rc) return rc;
+  if (n_iters_host) {
+    if (!check) {
+      *n_iters_host = max_iters;
+    } else {
+      int32_t v = 0;
+      if (hipMemcpyAsync(&v, L.ctrl + 1, sizeof(int32_t), hipMemcpyDeviceToHost,
+                         s) != hipSuccess ||
+          hipStreamSynchronize(s) != hipSuccess)
+        return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: reading iteration count failed");
+      *n_iters_host = v;
+    }
+  }
+  return FKC_OK;
+}
+
+void fkc_profile_enable(int enable) {
+  g_prof.enabled = enable != 0;
+  prof_clear_events();
+  g_prof.total_ms = 0.0;
+  g_prof.launches = 0;
+}
+
+int fkc_profile_assign_ms(double* total_ms, int64_t* launches) {
+  double tot = 0.0;
+  for (size_t i = 0; i < g_prof.starts.size(); ++i) {
+    if (hipEventSynchronize(g_prof.stops[i]) != hipSuccess)
+      return fail(FKC_ERR_LAUNCH, "profile: event sync failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, g_prof.starts[i], g_prof.stops[i]) != hipSuccess)
+      return fail(FKC_ERR_LAUNCH, "profile: elapsed time failed");
+    tot += ms;
+  }
+  g_prof.total_ms += tot;
+  g_prof.launches += (int64_t)g_prof.starts.size();
+  prof_clear_events();
+  if (total_ms) *total_ms = g_prof.total_ms;
+  if (launches) *launches = g_prof.launches;
+  return FKC_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,93 @@
+// Internal declarations shared by the gfx950 kernels and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "fkc.h"
+
+namespace fkc {
+
+// ---------------------------------------------------------------- errors
+// Record a printf-style message as this thread's last error; returns `code`.
+int fail(int code, const char* fmt, ...);
+// Map the sticky launch status after a kernel launch to an FKC status.
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------- sizes
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+inline size_t dtype_size(int dtype) { return dtype == FKC_F32 ? 4 : 2; }
+
+// Bump allocator over a caller-owned workspace.
+struct Carve {
+  char* base;
+  size_t used = 0;
+  explicit Carve(void* p) : base(static_cast<char*>(p)) {}
+  template <typename T>
+  T* take(size_t count) {
+    size_t off = used;
+    used = align_up(used + count * sizeof(T), 256);
+    return base ? reinterpret_cast<T*>(base + off) : nullptr;
+  }
+};
+
+// ---------------------------------------------------------------- assign
+// Routing predicate: the MFMA kernel serves fp16/bf16, D % 16 == 0, D <= 256.
+bool assign_uses_mfma(int dtype, int64_t D);
+int launch_assign(const void* x, const void* c, const float* x_sq,
+                  const float* c_sq, int32_t* ids, int64_t B, int64_t N,
+                  int64_t K, int64_t D, int dtype, const int32_t* ctrl,
+                  hipStream_t s);
+int launch_row_sqnorm(const void* src, float* out, int64_t rows, int64_t D,
+                      int dtype, const int32_t* ctrl, hipStream_t s);
+
+// ---------------------------------------------------------------- sort
+struct SortPlan {
+  int passes = 0;       // LSD passes (0 when K == 1)
+  int bits[4] = {0};    // digit width of each pass
+  int shift[4] = {0};   // bit offset of each pass
+  int64_t ntiles = 0;   // key tiles per batch row
+};
+// labels_valid: the caller guarantees every label is in [0,K), which saves
+// the sentinel bin (K = 256 then sorts in one 8-bit pass).
+SortPlan sort_plan(int64_t N, int64_t K, bool labels_valid);
+size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K);
+int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
+                      int64_t B, int64_t N, int64_t K, bool labels_valid,
+                      void* ws, size_t ws_bytes, const int32_t* ctrl,
+                      hipStream_t s);
+
+// ---------------------------------------------------------------- update
+size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D);
+// overwrite=false: sums/counts += run totals (caller zeroed them).
+// overwrite=true : every bin of sums/counts is written (absent bins get 0);
+//                  requires every label in [0,K) and sorted order.
+int launch_update(const void* x, const int32_t* perm /*nullable*/,
+                  const int32_t* ids_sorted, float* sums, int32_t* counts,
+                  int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
+                  bool overwrite, void* ws, size_t ws_bytes,
+                  const int32_t* ctrl, hipStream_t s);
+
+// ---------------------------------------------------------------- finalize
+// c_sq_out / shift_out may be null.  shift_out receives max over rows of
+// ||new-old||_2 through an atomic max (caller zeroes it).
+int launch_finalize(const float* sums, const int32_t* counts, const void* old,
+                    void* out, float* c_sq_out, float* shift_out, int64_t B,
+                    int64_t K, int64_t D, int dtype, const int32_t* ctrl,
+                    hipStream_t s);
+
+// ---------------------------------------------------------------- misc
+int launch_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
+// p[b*N + n] = n for every batch row b.
+int launch_iota_i32(int32_t* p, int64_t B, int64_t N, hipStream_t s);
+int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);
+int launch_converge_check(const float* shift, int it, float tol, int32_t* ctrl,
+                          hipStream_t s);
+
+// FKC_ASSIGN_FORCE_SAFE=1|true: route every dtype to the fp32 VALU kernel.
+bool force_safe_assign();
+// FKC_NTILES=1|2|4: point tiles (of 32) per wave in the MFMA kernel; 0 = auto.
+int ntiles_override();
+
+}  // namespace fkc

@@ -1,0 +1,125 @@
+"""Batched Euclidean K-Means driver (mirror of the reference's
+flash_kmeans_cuda/kmeans.py:108-195: same signature, return values and
+errors).
+
+The whole Lloyd loop runs in native code (fkc_kmeans_lloyd in libfkc.so):
+one call enqueues every iteration's assign -> label sort -> update ->
+finalize on torch's current stream.  With tol > 0 the convergence test runs
+on the device (finalize also produces the shift), so the host waits once, at
+the end, to learn the iteration count, instead of once per iteration as the
+reference's `shift.item()` does (kmeans.py:190).  verbose=True keeps the
+reference's per-iteration host loop so it can print every shift.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .ops import centroid_finalize, centroid_update_sorted, euclid_assign, row_sqnorm
+
+
+def _assign_reads_x_sq(x: torch.Tensor) -> bool:
+    """True when euclid_assign takes the fp32 route, which reads x_sq (the
+    counterpart of the reference's _can_skip_x_sq_for_assign, kmeans.py:48-70)."""
+    import os
+    force = os.environ.get("FKC_ASSIGN_FORCE_SAFE", "").lower() in ("1", "true")
+    D = x.shape[-1]
+    mfma = x.dtype in (torch.float16, torch.bfloat16) and D % 16 == 0 and D <= 256
+    return force or not mfma
+
+
+def _euclid_iter(x, x_sq, centroids, *, compute_shift=True, cluster_ids_buf=None,
+                 sums_buf=None, counts_buf=None, new_centroids_buf=None):
+    """One assign+update+finalize step (kmeans.py:73-105).
+    Returns (new_centroids, shift, cluster_ids)."""
+    B, K, D = centroids.shape
+    c_sq = row_sqnorm(centroids)
+    cluster_ids = euclid_assign(x, centroids, x_sq, c_sq=c_sq, out=cluster_ids_buf)
+    sums, counts = centroid_update_sorted(x, cluster_ids, K, sums_out=sums_buf,
+                                          counts_out=counts_buf)
+    new_centroids = centroid_finalize(sums, counts, centroids, out=new_centroids_buf)
+    shift = None
+    if compute_shift:
+        shift = (new_centroids.float() - centroids.float()).norm(dim=-1).max()
+    return new_centroids, shift, cluster_ids
+
+
+def batch_kmeans_Euclid(
+    x: torch.Tensor,
+    n_clusters: int,
+    max_iters: int = 100,
+    tol: float = 0.0,
+    init_centroids: Optional[torch.Tensor] = None,
+    verbose: bool = False,
+    *,
+    use_heuristic: bool = True,  # accepted for API parity, ignored
+) -> Tuple[torch.Tensor, torch.Tensor, int]:
+    """Batched K-Means clustering using Euclidean distance.
+
+    Args:
+        x: (B, N, D) fp16/bf16/fp32 CUDA tensor.
+        n_clusters: K.
+        max_iters: maximum number of iterations.
+        tol: convergence tolerance on the max centroid shift; <= 0 runs all
+            ``max_iters``.
+        init_centroids: optional (B, K, D) initial centroids (not modified).
+            If None, K random points of each batch row are used (sampled with
+            replacement, as the reference does).
+        verbose: print the shift of every iteration.
+        use_heuristic: ignored.
+
+    Returns:
+        (cluster_ids (B, N) int32, centroids (B, K, D) x.dtype, n_iters_run)
+    """
+    del use_heuristic
+    assert x.is_cuda, "flash_kmeans_cuda requires a CUDA input"
+    assert x.dim() == 3, "x must be (B, N, D)"
+    x = x.contiguous()
+    B, N, D = x.shape
+    K = int(n_clusters)
+
+    if init_centroids is None:
+        idx = torch.randint(0, N, (B, K), device=x.device)
+        centroids = torch.gather(x, dim=1, index=idx.unsqueeze(-1).expand(-1, -1, D))
+    else:
+        centroids = init_centroids.contiguous().view(B, K, D).clone()
+    if centroids.dtype != x.dtype:
+        raise RuntimeError("x and centroids must share dtype")
+    centroids = centroids.contiguous()
+
+    cluster_ids = torch.empty((B, N), device=x.device, dtype=torch.int32)
+
+    if verbose:
+        x_sq = (row_sqnorm(x) if _assign_reads_x_sq(x)
+                else torch.empty((B, N), device=x.device, dtype=torch.float32))
+        sums_buf = torch.empty((B, K, D), device=x.device, dtype=torch.float32)
+        counts_buf = torch.empty((B, K), device=x.device, dtype=torch.int32)
+        nxt = torch.empty_like(centroids)
+        cur = centroids
+        n_iters_run = 0
+        for it in range(max_iters):
+            new_c, shift, cluster_ids = _euclid_iter(
+                x, x_sq, cur, compute_shift=True, cluster_ids_buf=cluster_ids,
+                sums_buf=sums_buf, counts_buf=counts_buf, new_centroids_buf=nxt)
+            n_iters_run = it + 1
+            print(f"Iter {it}, center shift: {shift.item():.6f}")
+            if tol > 0 and shift.item() < tol:
+                cur = new_c
+                break
+            cur, nxt = nxt, cur
+        return cluster_ids, cur, n_iters_run
+
+    with torch.cuda.device(x.device):
+        dt = _lib.dtype_code(x.dtype)
+        ws = _lib.workspace(
+            _lib.lib.fkc_kmeans_workspace_bytes(B, N, K, D, dt, max(max_iters, 1)),
+            x.device)
+        n_host = _lib.ctypes.c_int32(0)
+        _lib.check(_lib.lib.fkc_kmeans_lloyd(
+            x.data_ptr(), centroids.data_ptr(), cluster_ids.data_ptr(), B, N, K, D, dt,
+            int(max_iters), float(tol), ws.data_ptr(), ws.numel(), _lib.stream_of(x),
+            None, _lib.ctypes.byref(n_host)), "batch_kmeans_Euclid")
+    return cluster_ids, centroids, int(n_host.value)

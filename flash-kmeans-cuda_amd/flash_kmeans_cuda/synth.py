@@ -1,0 +1,131 @@
+"""Seeded synthetic workloads of the benchmark configurations (CPU, numpy).
+
+Data is generated on the host with numpy's PCG64 generator, in float32, then
+rounded to the compute dtype, so a GPU run and a CPU check see identical
+bytes.  Draw order for one batch row (fixed; changing it changes the data):
+
+  rng  = default_rng(seed)
+  centres = 2 * rng.standard_normal((blobs, D), float32)      # N(0, 4 I)
+  blob    = rng.integers(0, blobs, N)            (uniform) or
+            rng.choice(blobs, N, p=zipf_probs)   (Zipf, p_k ∝ (k+1)^-s)
+  noise   = sigma * rng.standard_normal((N, D), float32)
+  x       = round_to_dtype(centres[blob] + noise)
+  init    = x[default_rng(init_seed).choice(N, K, replace=False)]
+
+The "plumbing" config draws x = standard_normal((N, D)) from seed 0 instead.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    B: int
+    N: int
+    K: int
+    D: int
+    dtype: str           # "f32" | "f16" | "bf16"
+    iters: int
+    tol: float
+    kind: str            # "normal" | "mixture"
+    sigma: float = 0.5
+    zipf: Optional[float] = None
+    seed: int = 0        # data seed of batch row 0 (row b uses seed + b when per_batch_seed)
+    init_seed: int = 1
+    per_batch_seed: bool = False
+
+
+CONFIGS = {
+    "c1": Config("c1_plumbing_f32", 1, 4096, 64, 128, "f32", 10, 0.0, "normal"),
+    "c2": Config("c2_f16_k256", 1, 32768, 256, 128, "f16", 10, 0.0, "mixture"),
+    "c3": Config("c3_f16_k2048", 1, 131072, 2048, 128, "f16", 10, 0.0, "mixture"),
+    "c4": Config("c4_bf16_b8_k1024_d64", 8, 65536, 1024, 64, "bf16", 15, 1e-4,
+                 "mixture", seed=0, init_seed=100, per_batch_seed=True),
+    "c5": Config("c5_f16_k8192_zipf", 1, 524288, 8192, 128, "f16", 10, 0.0,
+                 "mixture", zipf=1.1),
+}
+
+
+def f32_to_bf16_bits(f: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(f, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = np.where(nan, 0x7FC0, (u + 0x7FFF + ((u >> 16) & 1)) >> 16)
+    return r.astype(np.uint16)
+
+
+def round_to(f: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 -> storage array (f16: numpy float16, bf16: uint16 bits)."""
+    if dtype == "f32":
+        return np.ascontiguousarray(f, dtype=np.float32)
+    if dtype == "f16":
+        return f.astype(np.float16)
+    if dtype == "bf16":
+        return f32_to_bf16_bits(f)
+    raise ValueError(dtype)
+
+
+def zipf_probs(n: int, s: float) -> np.ndarray:
+    p = np.arange(1, n + 1, dtype=np.float64) ** (-s)
+    return p / p.sum()
+
+
+def make_row(cfg: Config, seed: int, N: Optional[int] = None) -> np.ndarray:
+    """One batch row of x as float32 before rounding, (N, D)."""
+    N = cfg.N if N is None else N
+    rng = np.random.default_rng(seed)
+    if cfg.kind == "normal":
+        return rng.standard_normal((N, cfg.D), dtype=np.float32)
+    blobs = cfg.K
+    centres = 2.0 * rng.standard_normal((blobs, cfg.D), dtype=np.float32)
+    if cfg.zipf is None:
+        blob = rng.integers(0, blobs, N)
+    else:
+        blob = rng.choice(blobs, N, p=zipf_probs(blobs, cfg.zipf))
+    noise = rng.standard_normal((N, cfg.D), dtype=np.float32)
+    noise *= np.float32(cfg.sigma)
+    out = centres[blob]
+    out += noise
+    return out
+
+
+def make(cfg: Config, N: Optional[int] = None):
+    """(x, init) storage arrays of shapes (B,N,D) and (B,K,D)."""
+    N = cfg.N if N is None else N
+    xs, inits = [], []
+    for b in range(cfg.B):
+        seed = cfg.seed + b if cfg.per_batch_seed else cfg.seed
+        iseed = cfg.init_seed + b if cfg.per_batch_seed else cfg.init_seed
+        xb = round_to(make_row(cfg, seed, N), cfg.dtype)
+        idx = np.random.default_rng(iseed).choice(N, cfg.K, replace=False)
+        xs.append(xb)
+        inits.append(xb[idx])
+    return np.stack(xs), np.stack(inits)
+
+
+def to_torch(a: np.ndarray, dtype: str, device="cuda"):
+    """Storage array -> torch tensor of the compute dtype on `device`."""
+    import torch
+    if dtype == "bf16":
+        t = torch.from_numpy(a.astype(np.int16, copy=False).view(np.int16)).view(torch.bfloat16)
+    elif dtype == "f16":
+        t = torch.from_numpy(a)
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    return t.to(device)
+
+
+def from_torch(t, dtype: str) -> np.ndarray:
+    """torch tensor of the compute dtype -> storage array."""
+    import torch
+    t = t.detach().cpu().contiguous()
+    if dtype == "bf16":
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if dtype == "f16":
+        return t.numpy()
+    return t.float().numpy()

@@ -1,0 +1,167 @@
+/*
+ * fkc.h — C ABI of the MI355X (gfx950) K-Means hot path.
+ *
+ * Batched Euclidean Lloyd iterations: assign -> stable label sort ->
+ * indexed centroid update -> finalize.  Every entry point:
+ *   - takes plain device pointers, element counts and a HIP stream
+ *     (NULL = the null stream); nothing here knows about torch types;
+ *   - enqueues asynchronously on that stream and never synchronises,
+ *     except fkc_kmeans_lloyd when the caller asks for the host
+ *     iteration count (see there);
+ *   - allocates no device memory: scratch comes in through a caller-owned
+ *     workspace whose size the matching *_workspace_bytes() reports;
+ *   - returns FKC_OK (0) or a non-zero FKC_ERR_* code and never throws;
+ *     fkc_last_error() then gives a message (thread-local).
+ *
+ * Layouts are the reference's: x (B,N,D) row-major, centroids (B,K,D),
+ * ids (B,N) int32, sums (B,K,D) fp32, counts (B,K) int32, x_sq (B,N) fp32,
+ * c_sq (B,K) fp32.  Element type is one of FKC_F32 / FKC_F16 / FKC_BF16.
+ *
+ * Reference interfaces replaced (OpsiClear/flash-kmeans-cuda):
+ *   flash_kmeans_cuda/csrc/flash_kmeans_cuda.h:33-75  (fkc:: libtorch API)
+ *   flash_kmeans_cuda/csrc/bindings.cpp:107-127        (_C extension module)
+ *   flash_kmeans_cuda/kmeans.py:108-195                (Lloyd driver loop)
+ *   flash_kmeans_cuda/ops.py:58-112                    (torch.sort call site)
+ */
+#ifndef FKC_H_
+#define FKC_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(_WIN32)
+#define FKC_CAPI __declspec(dllexport)
+#else
+#define FKC_CAPI __attribute__((visibility("default")))
+#endif
+
+/* Same type as hipStream_t (struct ihipStream_t*); NULL is the null stream. */
+typedef struct ihipStream_t* fkc_stream_t;
+
+enum fkc_status {
+  FKC_OK = 0,
+  FKC_ERR_INVALID = 1,     /* bad argument: shape, dtype, null pointer */
+  FKC_ERR_WORKSPACE = 2,   /* workspace missing or smaller than required */
+  FKC_ERR_LAUNCH = 3,      /* a HIP launch or runtime call failed */
+  FKC_ERR_UNSUPPORTED = 4  /* valid request this build cannot serve */
+};
+
+enum fkc_dtype { FKC_F32 = 0, FKC_F16 = 1, FKC_BF16 = 2 };
+
+/* Message for the last failing call on this thread ("" if none). */
+FKC_CAPI const char* fkc_last_error(void);
+/* Library version string, e.g. "0.1.0". */
+FKC_CAPI const char* fkc_version(void);
+
+/*
+ * Nearest-centroid assignment: ids[b,n] = argmin_k ||x[b,n]-c[b,k]||^2,
+ * the lowest k winning exact ties.
+ * Replaces fkc::euclid_assign_out (flash_kmeans_cuda.h:41-46, api.cpp:58-72)
+ * and _C.euclid_assign (bindings.cpp:43-63).
+ *   - fp16/bf16 with D % 16 == 0 and D <= 256: MFMA kernel ranking
+ *     c_sq[k] - 2<x,c_k> in fp32 (x_sq is not read; like the reference's
+ *     raw-distance route, assign_sm80.cu:437-441, 687).
+ *   - every other case, and FKC_ASSIGN_FORCE_SAFE=1: fp32 VALU kernel ranking
+ *     max(0, x_sq + c_sq - 2<x,c>) (assign_safe.cu:55-80,
+ *     assign_common.cuh:33-36).  x_sq may be NULL: then it is computed.
+ * c_sq must hold the fp32 squared norms of the centroids as stored.
+ */
+FKC_CAPI int fkc_euclid_assign(const void* x, const void* centroids,
+                               const float* x_sq, const float* c_sq,
+                               int32_t* cluster_ids, int64_t B, int64_t N,
+                               int64_t K, int64_t D, int dtype,
+                               fkc_stream_t stream);
+
+/* out[r] = sum_d float(src[r,d])^2 for r < rows.  Replaces the torch
+ * expressions (c.float()**2).sum(-1) at kmeans.py:94 and x.float()**2 at
+ * kmeans.py:151. */
+FKC_CAPI int fkc_row_sqnorm(const void* src, float* out, int64_t rows,
+                            int64_t D, int dtype, fkc_stream_t stream);
+
+/*
+ * Stable sort of the labels of each batch row: sorted_ids[b,:] ascending,
+ * perm[b,p] the original index of sorted position p, equal labels in index
+ * order.  Labels outside [0,K) sort after every valid label, in index order.
+ * Replaces torch.sort(cluster_ids, dim=1) at ops.py:89 (the reference asks
+ * stable=False; this sort is always stable).
+ */
+FKC_CAPI size_t fkc_label_sort_workspace_bytes(int64_t B, int64_t N,
+                                               int64_t K);
+FKC_CAPI int fkc_label_sort(const int32_t* cluster_ids, int32_t* sorted_ids,
+                            int32_t* perm, int64_t B, int64_t N, int64_t K,
+                            void* workspace, size_t workspace_bytes,
+                            fkc_stream_t stream);
+
+/*
+ * Centroid accumulation over label-sorted rows.  Adds into sums/counts
+ * (the caller zeroes them first, as _C.centroid_update_sorted expects,
+ * bindings.cpp:65-79); labels outside [0,K) are skipped
+ * (update_sorted.cu:95,167).  ids_sorted must be non-decreasing over the
+ * valid labels of each batch row.  Summation is fp32, in sorted order within
+ * a run, and deterministic: the same inputs give the same bits.
+ * _sorted reads x_sorted row p for sorted position p (update_sorted.cu:39-116);
+ * _indexed reads x row sorted_idx[p] (update_sorted.cu:118-186).
+ */
+FKC_CAPI size_t fkc_update_workspace_bytes(int64_t B, int64_t N, int64_t D);
+FKC_CAPI int fkc_centroid_update_sorted(const void* x_sorted,
+                                        const int32_t* ids_sorted, float* sums,
+                                        int32_t* counts, int64_t B, int64_t N,
+                                        int64_t K, int64_t D, int dtype,
+                                        void* workspace, size_t workspace_bytes,
+                                        fkc_stream_t stream);
+FKC_CAPI int fkc_centroid_update_sorted_indexed(
+    const void* x, const int32_t* sorted_idx, const int32_t* ids_sorted,
+    float* sums, int32_t* counts, int64_t B, int64_t N, int64_t K, int64_t D,
+    int dtype, void* workspace, size_t workspace_bytes, fkc_stream_t stream);
+
+/*
+ * out[b,k,:] = counts[b,k] > 0 ? cast(sums[b,k,:] / counts[b,k]) : old[b,k,:]
+ * (IEEE division, round-to-nearest-even cast).  out may alias old.
+ * Replaces fkc::centroid_finalize_out (flash_kmeans_cuda.h:71-75) and
+ * launch_centroid_finalize (update_finalize.cu:39-121).
+ */
+FKC_CAPI int fkc_centroid_finalize(const float* sums, const int32_t* counts,
+                                   const void* old_centroids, void* out,
+                                   int64_t B, int64_t K, int64_t D, int dtype,
+                                   fkc_stream_t stream);
+
+/*
+ * Whole Lloyd loop of batch_kmeans_Euclid (kmeans.py:108-195) in one call.
+ * centroids (B,K,D) holds the initial centroids on entry and the final ones
+ * on return (updated in place); cluster_ids receives the labels of the last
+ * assignment, made against the centroids before the last update
+ * (kmeans.py:179-195).  With tol > 0 the loop stops after the first
+ * iteration whose max centroid shift max_{b,k} ||new-old||_2 is below tol
+ * (kmeans.py:104,190); the test runs on the device, so no host sync is
+ * needed between iterations.  n_iters_dev (device int32, may be NULL)
+ * receives the iterations run.  n_iters_host (may be NULL): when tol > 0 the
+ * call synchronises the stream to fill it; when tol <= 0 it is max_iters.
+ */
+FKC_CAPI size_t fkc_kmeans_workspace_bytes(int64_t B, int64_t N, int64_t K,
+                                           int64_t D, int dtype,
+                                           int max_iters);
+FKC_CAPI int fkc_kmeans_lloyd(const void* x, void* centroids,
+                              int32_t* cluster_ids, int64_t B, int64_t N,
+                              int64_t K, int64_t D, int dtype, int max_iters,
+                              float tol, void* workspace,
+                              size_t workspace_bytes, fkc_stream_t stream,
+                              int32_t* n_iters_dev, int32_t* n_iters_host);
+
+/*
+ * Profiling hook for benchmarks (no counterpart in the reference): when
+ * enabled, fkc_kmeans_lloyd brackets every assignment launch with HIP events
+ * on its stream.  fkc_profile_assign_ms() synchronises on the recorded events
+ * and returns the summed assignment time in ms and the launch count.
+ */
+FKC_CAPI void fkc_profile_enable(int enable);
+FKC_CAPI int fkc_profile_assign_ms(double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FKC_H_ */

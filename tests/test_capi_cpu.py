@@ -1,0 +1,132 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+declared in include/fkc.h, and rejects bad arguments with a status code and a
+message before touching the device.  Also the host-side Python wrappers'
+argument checks (ValueError / RuntimeError / AssertionError as in the
+reference: ops.py:23-24, kmeans.py:141-142, TORCH_CHECK -> RuntimeError)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fkc.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"FKC_CAPI\s+[\w\s\*]+?\b(fkc_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_surface():
+    names = _declared()
+    for n in ["fkc_euclid_assign", "fkc_row_sqnorm", "fkc_label_sort",
+              "fkc_label_sort_workspace_bytes", "fkc_centroid_update_sorted",
+              "fkc_centroid_update_sorted_indexed", "fkc_update_workspace_bytes",
+              "fkc_centroid_finalize", "fkc_kmeans_lloyd", "fkc_kmeans_workspace_bytes",
+              "fkc_last_error", "fkc_version"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from flash_kmeans_cuda import _lib
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert missing == []
+    assert set(_declared()) <= set(_lib.SIGNATURES)
+
+
+def test_version_matches_package():
+    import flash_kmeans_cuda
+    from flash_kmeans_cuda import _lib
+    assert _lib.lib.fkc_version().decode() == flash_kmeans_cuda.__version__
+
+
+def _err(rc):
+    from flash_kmeans_cuda import _lib
+    return rc, _lib.last_error()
+
+
+def test_invalid_arguments_are_rejected_without_a_device():
+    from flash_kmeans_cuda import _lib
+    L = _lib.lib
+    fake = 0x1000  # never dereferenced: validation fails first
+    rc, msg = _err(L.fkc_euclid_assign(fake, fake, None, fake, fake, 1, 10, 0, 16, 1, None))
+    assert rc == 1 and "K>=1" in msg
+    rc, msg = _err(L.fkc_euclid_assign(fake, fake, None, fake, fake, 1, 10, 4, 16, 7, None))
+    assert rc == 1 and "dtype" in msg
+    rc, msg = _err(L.fkc_euclid_assign(None, fake, None, fake, fake, 1, 10, 4, 16, 1, None))
+    assert rc == 1 and "null" in msg
+    rc, msg = _err(L.fkc_label_sort(fake, fake, fake, 1, 1000, 10, None, 0, None))
+    assert rc == 2 and "workspace" in msg
+    rc, msg = _err(L.fkc_centroid_update_sorted_indexed(fake, None, fake, fake, fake,
+                                                        1, 10, 4, 8, 1, None, 0, None))
+    assert rc == 1 and "sorted_idx" in msg
+    rc, msg = _err(L.fkc_centroid_update_sorted(fake, fake, fake, fake, 1, 10, 4, 8, 1,
+                                                None, 0, None))
+    assert rc == 2
+    rc, msg = _err(L.fkc_kmeans_lloyd(fake, fake, fake, 1, 100, 4, 8, 1, 3, 0.0, None, 0,
+                                      None, None, None))
+    assert rc == 2 and "workspace" in msg
+    rc, msg = _err(L.fkc_kmeans_lloyd(fake, fake, fake, 1, 100, 4, 8, 1, -1, 0.0, None, 0,
+                                      None, None, None))
+    assert rc == 1
+    rc, msg = _err(L.fkc_centroid_finalize(None, fake, fake, fake, 1, 4, 8, 1, None))
+    assert rc == 1
+    assert L.fkc_euclid_assign(fake, fake, None, fake, fake, 1 << 20, 10, 4, 16, 1, None) == 4
+
+
+def test_empty_inputs_are_no_ops():
+    from flash_kmeans_cuda import _lib
+    L = _lib.lib
+    assert L.fkc_euclid_assign(None, None, None, None, None, 0, 0, 4, 16, 1, None) == 0
+    assert L.fkc_label_sort(None, None, None, 1, 0, 4, None, 0, None) == 0
+    n = ctypes.c_int32(-1)
+    assert L.fkc_kmeans_lloyd(None, None, None, 1, 100, 4, 8, 1, 0, 0.0, None, 0, None,
+                              None, ctypes.byref(n)) == 0
+    assert n.value == 0
+
+
+def test_workspace_sizes():
+    from flash_kmeans_cuda import _lib
+    L = _lib.lib
+    # mega config: sort needs a 256-bin table per 4096-key tile plus one
+    # key/payload ping buffer (two 13/14-bit passes)
+    s = L.fkc_label_sort_workspace_bytes(1, 524288, 8192)
+    assert 2 * 524288 * 4 <= s < 3 * 524288 * 4
+    assert L.fkc_label_sort_workspace_bytes(1, 4096, 255) < 4 * 4096 * 4
+    u = L.fkc_update_workspace_bytes(1, 524288, 128)
+    assert u >= 4096 * 2 * 128 * 4
+    k = L.fkc_kmeans_workspace_bytes(1, 524288, 8192, 128, 1, 10)
+    assert k > s + u + 8192 * 128 * 4
+    # the fp32 route needs x_sq as well
+    assert (L.fkc_kmeans_workspace_bytes(1, 4096, 64, 128, 0, 10)
+            - L.fkc_kmeans_workspace_bytes(1, 4096, 64, 128, 1, 10)) >= 4096 * 4
+
+
+def test_python_wrappers_reject_bad_arguments():
+    from flash_kmeans_cuda import _C, batch_kmeans_Euclid, euclid_assign
+    x = torch.randn(1, 10, 16)
+    with pytest.raises(ValueError):
+        euclid_assign(x, x[:, :2], (x ** 2).sum(-1))
+    with pytest.raises(AssertionError):
+        batch_kmeans_Euclid(x, 2, max_iters=1)
+    with pytest.raises(RuntimeError):
+        _C.euclid_assign(x, x[:, :2], (x ** 2).sum(-1), (x[:, :2] ** 2).sum(-1))
+
+
+def test_synth_generators_are_deterministic():
+    from flash_kmeans_cuda import synth
+    cfg = synth.CONFIGS["c4"]
+    a, ia = synth.make(cfg, N=2048)
+    b, ib = synth.make(cfg, N=2048)
+    assert a.dtype == np.uint16 and a.shape == (8, 2048, 64) and ia.shape == (8, 1024, 64)
+    assert np.array_equal(a, b) and np.array_equal(ia, ib)
+    assert not np.array_equal(a[0], a[1])  # per-batch seeds
+    p = synth.zipf_probs(8192, 1.1)
+    assert abs(p.sum() - 1) < 1e-12 and 0.14 < p[0] < 0.16

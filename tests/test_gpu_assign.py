@@ -1,0 +1,159 @@
+"""GPU parity of the assignment kernels against the oracle (through the C ABI).
+
+Bar: labels identical to the exact-distance oracle except on near-ties
+(exact distance gap <= 2^-16 of ||x||^2 + ||c||^2, what an fp32-accumulated
+score can misjudge), and near-ties under 0.1% of points at sizes where that
+fraction is meaningful.  Integer outcomes that do not depend on rounding
+(identity centroids, duplicate centroids, determinism, tile-count
+invariance) must be bit-exact.  Cases mirror the reference's tests:
+tests/test_mma_optin.py:35-68, tests/test_shapes.py:11-53,
+tests/test_persistent.py:97-165, tests/cpp/smoke.cpp:31-53.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import near_tie_report
+from oracle import kmeans_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _data(B, N, K, D, dtype, seed=0, scale=1.0):
+    rng = np.random.default_rng(seed)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32) * scale, dtype)
+    c = O.from_f32(rng.standard_normal((B, K, D)).astype(np.float32) * scale, dtype)
+    return x, c
+
+
+def _gpu_assign(x, c, dtype, with_xsq=True):
+    from flash_kmeans_cuda import _C, synth
+    from flash_kmeans_cuda.ops import row_sqnorm
+    xt = synth.to_torch(x, dtype)
+    ct = synth.to_torch(c, dtype)
+    x_sq = row_sqnorm(xt) if with_xsq else torch.empty(0, device="cuda")
+    ids = _C.euclid_assign(xt, ct, x_sq, row_sqnorm(ct))
+    torch.cuda.synchronize()
+    return ids.cpu().numpy()
+
+
+def _check(x, c, dtype, got, max_frac=None):
+    ref = O.assign(x, c, dtype)
+    nd, bad, worst = near_tie_report(x, c, dtype, got, ref)
+    assert bad == 0, f"{bad} non-near-tie disagreements (worst rel gap {worst:.3e})"
+    if max_frac is not None:
+        assert nd / got.size < max_frac, f"{nd}/{got.size} near-tie flips"
+    return nd
+
+
+MFMA_CASES = [
+    (1, 1024, 64, 64), (1, 4096, 128, 128), (2, 8192, 256, 128),   # test_mma_optin
+    (1, 100, 8, 64), (1, 257, 16, 128), (1, 1024, 1, 64), (1, 1024, 63, 64),
+    (1, 1024, 65, 64), (1, 1024, 32, 256), (3, 2048, 32, 64),       # test_shapes
+    (1, 256, 2048, 128), (1, 777, 129, 128),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("B,N,K,D", MFMA_CASES)
+def test_mfma_assign_matches_oracle(dtype, B, N, K, D):
+    x, c = _data(B, N, K, D, dtype, seed=B * N + K + D)
+    got = _gpu_assign(x, c, dtype)
+    _check(x, c, dtype, got, max_frac=1e-3 if B * N >= 4096 else None)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("D", [16 * s for s in range(1, 17)])
+def test_mfma_every_feature_width(dtype, D):
+    x, c = _data(1, 300, 97, D, dtype, seed=D)
+    _check(x, c, dtype, _gpu_assign(x, c, dtype))
+
+
+@pytest.mark.parametrize("ntiles", ["1", "2", "4"])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_identity_centroids_and_tail(monkeypatch, ntiles, dtype):
+    """First K rows as centroids map to themselves (test_persistent.py:35-64)."""
+    monkeypatch.setenv("FKC_NTILES", ntiles)
+    for (N, K, D) in [(4096, 64, 128), (257, 16, 128), (8192, 128, 64)]:
+        x, _ = _data(1, N, 1, D, dtype, seed=N)
+        c = x[:, :K].copy()
+        got = _gpu_assign(x, c, dtype)
+        assert np.array_equal(got[0, :K], np.arange(K))
+        assert got.min() >= 0 and got.max() < K
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_duplicate_centroids_take_lowest_index(dtype):
+    x, c = _data(2, 3000, 96, 128, dtype, seed=11)
+    c[:, 70] = c[:, 5]
+    c[:, 95] = c[:, 5]
+    c[:, 40] = c[:, 39]
+    got = _gpu_assign(x, c, dtype)
+    assert not np.isin(got, [70, 95, 40]).any()
+    _check(x, c, dtype, got)
+
+
+def test_exact_ties_take_lowest_index():
+    # Every point is the origin; centroids at equal distance -> index 1.
+    x = np.zeros((1, 500, 64), dtype=np.float16)
+    c = np.zeros((1, 40, 64), dtype=np.float32)
+    c[0, 0, 0] = 2.0
+    c[0, 1:, :] = 0.0
+    for k in range(1, 40):
+        c[0, k, k % 64] = 1.0 if k % 2 else -1.0
+    c = c.astype(np.float16)
+    for dtype, xs, cs in [("f16", x, c), ("f32", x.astype(np.float32), c.astype(np.float32))]:
+        got = _gpu_assign(xs, cs, dtype)
+        assert np.all(got == 1), np.unique(got)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_determinism_and_ntiles_invariance(monkeypatch, dtype):
+    """Repeated launches and every tile count give bit-identical labels
+    (test_persistent.py:97-165 asks determinism and <1% drift; the scores here
+    do not depend on the tiling, so equality is required)."""
+    x, c = _data(1, 32768, 256, 128, dtype, seed=3)
+    outs = []
+    for nt in ["1", "2", "4", "1"]:
+        monkeypatch.setenv("FKC_NTILES", nt)
+        outs.append(_gpu_assign(x, c, dtype))
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("B,N,K,D", [(1, 4096, 64, 128), (2, 1000, 33, 37), (1, 513, 300, 16)])
+def test_fp32_route_matches_oracle(B, N, K, D):
+    x, c = _data(B, N, K, D, "f32", seed=N + D)
+    got = _gpu_assign(x, c, "f32")
+    _check(x, c, "f32", got, max_frac=1e-3 if B * N >= 4096 else None)
+
+
+@pytest.mark.parametrize("D", [1, 7, 31, 48, 257, 300])
+def test_fp16_odd_widths_use_fp32_route(D):
+    """D % 16 != 0 or D > 256 fall back to the fp32 kernel (smoke.cpp:104)."""
+    x, c = _data(1, 512, 64, D, "f16", seed=D)
+    got = _gpu_assign(x, c, "f16")
+    _check(x, c, "f16", got)
+    got2 = _gpu_assign(x, c, "f16", with_xsq=False)  # x_sq computed in-kernel
+    assert np.array_equal(got, got2)
+
+
+def test_force_safe_env_routes_to_fp32_kernel(monkeypatch):
+    x, c = _data(1, 2048, 128, 128, "f16", seed=21)
+    monkeypatch.setenv("FKC_ASSIGN_FORCE_SAFE", "1")
+    got = _gpu_assign(x, c, "f16")
+    _check(x, c, "f16", got)
+
+
+def test_clustered_data_large_k():
+    """Gaussian-mixture data at K=8192 (the mega route), N scaled down."""
+    from flash_kmeans_cuda import synth
+    cfg = synth.CONFIGS["c5"]
+    x, init = synth.make(cfg, N=16384)
+    rng = np.random.default_rng(0)
+    c = x[:, rng.choice(16384, 8192, replace=False)].copy()
+    got = _gpu_assign(x, c, "f16")
+    _check(x, c, "f16", got, max_frac=1e-3)

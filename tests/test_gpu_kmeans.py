@@ -1,0 +1,237 @@
+"""GPU parity of the whole Lloyd loop (batch_kmeans_Euclid) against the oracle.
+
+* Lockstep: every iteration the GPU kernels and the oracle start from the
+  same centroids, so a near-tie flip cannot cascade: labels must agree up to
+  near-ties, the sort/counts are bit-exact given the GPU labels, the sums
+  agree to fp32 accumulation error and finalize is bit-exact given the GPU
+  sums.
+* End to end: labels < 0.1% disagreement, final inertia
+  within +-0.05%, centroid drift within 1e-2 relative.
+* Driver contract (kmeans.py:108-195): n_iters, tol, shapes, dtypes, init not
+  modified, verbose path == fused path; reference test cases
+  tests/test_shapes.py, tests/test_dtypes.py, tests/test_correctness.py.
+* Full-size C5 run checked through size-independent properties.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import inertia, near_tie_report
+from oracle import kmeans_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _T(a, dtype):
+    from flash_kmeans_cuda import synth
+    return synth.to_torch(a, dtype)
+
+
+def _N(t, dtype):
+    from flash_kmeans_cuda import synth
+    torch.cuda.synchronize()
+    return synth.from_torch(t, dtype)
+
+
+def _lockstep(x, init, K, dtype, iters):
+    from flash_kmeans_cuda import _C
+    from flash_kmeans_cuda.ops import label_sort, row_sqnorm
+    xt = _T(x, dtype)
+    cur = init.copy()
+    flips = 0
+    for it in range(iters):
+        ct = _T(cur, dtype)
+        ids_t = _C.euclid_assign(xt, ct, row_sqnorm(xt), row_sqnorm(ct))
+        ids = ids_t.cpu().numpy()
+        ref = O.assign(x, cur, dtype)
+        nd, bad, worst = near_tie_report(x, cur, dtype, ids, ref)
+        assert bad == 0, f"iter {it}: {bad} non-near-tie flips (worst {worst:.2e})"
+        flips += nd
+        s_t, p_t = label_sort(ids_t, K)
+        es, ep = O.label_sort(ids, K)
+        assert np.array_equal(p_t.cpu().numpy(), ep) and np.array_equal(s_t.cpu().numpy(), es)
+        sums = torch.zeros((x.shape[0], K, x.shape[2]), device="cuda")
+        cnt = torch.zeros((x.shape[0], K), device="cuda", dtype=torch.int32)
+        _C.centroid_update_sorted_indexed(xt, p_t, s_t, sums, cnt)
+        osum, ocnt = O.update_sorted_indexed(x, ep, es, K, dtype)
+        g_cnt = cnt.cpu().numpy()
+        g_sum = sums.cpu().numpy()
+        assert np.array_equal(g_cnt, ocnt), f"iter {it}: counts"
+        scale = np.abs(O.to_f64(x, dtype)).max() * np.maximum(ocnt, 1)[..., None]
+        assert np.all(np.abs(g_sum - osum) <= 1e-6 * scale + 1e-6), f"iter {it}: sums"
+        new_t = _C.centroid_finalize(sums, cnt, ct)
+        g_new = _N(new_t, dtype)
+        assert np.array_equal(np.asarray(g_new).view(np.uint8),
+                              np.asarray(O.finalize(g_sum, g_cnt, cur, dtype)).view(np.uint8))
+        cur = g_new
+    return flips
+
+
+@pytest.mark.parametrize("cfg_name,N", [("c2", 32768), ("c3", 32768), ("c4", 8192), ("c1", 4096)])
+def test_lockstep_iterations(cfg_name, N):
+    from flash_kmeans_cuda import synth
+    cfg = synth.CONFIGS[cfg_name]
+    x, init = synth.make(cfg, N=N)
+    flips = _lockstep(x, init, cfg.K, cfg.dtype, iters=3)
+    assert flips / (x.shape[0] * N * 3) < 1e-3
+
+
+def _end_to_end(cfg_name, N=None, iters=None):
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    cfg = synth.CONFIGS[cfg_name]
+    x, init = synth.make(cfg, N=N)
+    iters = cfg.iters if iters is None else iters
+    ids_t, c_t, n = batch_kmeans_Euclid(_T(x, cfg.dtype), cfg.K, max_iters=iters,
+                                        tol=cfg.tol, init_centroids=_T(init, cfg.dtype))
+    ids = ids_t.cpu().numpy()
+    cents = _N(c_t, cfg.dtype)
+    o_ids, o_c, o_n = O.kmeans(x, cfg.K, iters, cfg.tol, init, cfg.dtype)
+    return cfg, x, ids, cents, n, o_ids, o_c, o_n
+
+
+@pytest.mark.parametrize("cfg_name,N", [("c2", None), ("c1", None), ("c4", 16384)])
+def test_end_to_end_north_star_bar(cfg_name, N):
+    cfg, x, ids, cents, n, o_ids, o_c, o_n = _end_to_end(cfg_name, N)
+    assert n == o_n
+    frac = float((ids != o_ids).mean())
+    assert frac < 1e-3, f"label disagreement {frac:.4%}"
+    gi = inertia(x, cents, cfg.dtype, O.assign(x, cents, cfg.dtype))
+    oi = inertia(x, o_c, cfg.dtype, O.assign(x, o_c, cfg.dtype))
+    assert abs(gi - oi) / oi < 5e-4, f"inertia {gi} vs {oi}"
+    gc, oc = O.to_f64(cents, cfg.dtype), O.to_f64(o_c, cfg.dtype)
+    drift = np.linalg.norm(gc - oc) / np.linalg.norm(oc)
+    assert drift < 1e-2, f"centroid drift {drift:.3e}"
+
+
+def test_c1_golden_fixture():
+    """The fp32 plumbing config against the committed oracle output."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    z = np.load(os.path.join(GOLDEN, "c1.npz"))
+    cfg = synth.CONFIGS["c1"]
+    x, init = synth.make(cfg)
+    ids_t, c_t, n = batch_kmeans_Euclid(_T(x, "f32"), cfg.K, max_iters=10, tol=0.0,
+                                        init_centroids=_T(init, "f32"))
+    assert n == int(z["n_iters"])
+    ids = ids_t.cpu().numpy()[0]
+    assert (ids != z["labels"]).mean() < 1e-3
+    c = c_t.cpu().numpy()[0]
+    assert np.linalg.norm(c - z["centroids"]) / np.linalg.norm(z["centroids"]) < 1e-2
+
+
+def test_tiny_golden_fixtures_on_gpu():
+    from flash_kmeans_cuda import _C
+    from flash_kmeans_cuda.ops import row_sqnorm
+    z = np.load(os.path.join(GOLDEN, "tiny.npz"))
+    n = len([k for k in z.files if k.endswith("_dtype")])
+    for i in range(n):
+        dtype = str(z[f"{i}_dtype"])
+        x, c, ref = z[f"{i}_x"], z[f"{i}_c"], z[f"{i}_ids"]
+        xt, ct = _T(x, dtype), _T(c, dtype)
+        got = _C.euclid_assign(xt, ct, row_sqnorm(xt), row_sqnorm(ct)).cpu().numpy()
+        nd, bad, worst = near_tie_report(x, c, dtype, got, ref)
+        assert bad == 0, (i, dtype, worst)
+
+
+@pytest.mark.parametrize("B,N,K,D", [(1, 100, 8, 64), (1, 257, 16, 128), (1, 1024, 1, 64),
+                                     (1, 1024, 63, 64), (1, 1024, 65, 64), (1, 1024, 32, 256),
+                                     (3, 2048, 32, 64)])
+def test_shapes_contract(B, N, K, D):
+    """tests/test_shapes.py:11-31 of the reference."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    x = torch.randn(B, N, D, device="cuda", dtype=torch.float16)
+    ids, cents, n_iters = batch_kmeans_Euclid(x, K, max_iters=3, tol=0.0)
+    assert ids.shape == (B, N) and ids.dtype == torch.int32
+    assert cents.shape == (B, K, D) and cents.dtype == torch.float16
+    assert n_iters == 3
+    assert (ids >= 0).all() and (ids < K).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_dtypes_contract(dtype):
+    """tests/test_dtypes.py:11-42 of the reference."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid, euclid_assign
+    x = torch.randn(2, 2048, 64, device="cuda", dtype=dtype)
+    ids, cents, n = batch_kmeans_Euclid(x, 32, max_iters=5, tol=0.0)
+    assert cents.dtype == dtype and n == 5
+    x1 = torch.randn(1, 1024, 64, device="cuda", dtype=dtype)
+    a = euclid_assign(x1, x1[:, :32].contiguous(), (x1.float() ** 2).sum(-1))
+    assert a.dtype == torch.int32 and (a >= 0).all() and (a < 32).all()
+    s = torch.randn(1, 64, 32, device="cuda", dtype=torch.float16)
+    u = euclid_assign(s, s.clone(), (s.float() ** 2).sum(-1))
+    assert u.unique().numel() > 16
+
+
+def test_tol_stops_early_and_matches_truncated_run():
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    cfg = synth.CONFIGS["c4"]
+    x, init = synth.make(cfg, N=8192)
+    xt, it = _T(x, "bf16"), _T(init, "bf16")
+    ids_a, c_a, n_a = batch_kmeans_Euclid(xt, cfg.K, max_iters=50, tol=1e-2, init_centroids=it)
+    assert 1 <= n_a < 50
+    ids_b, c_b, n_b = batch_kmeans_Euclid(xt, cfg.K, max_iters=n_a, tol=0.0, init_centroids=it)
+    assert n_b == n_a
+    assert torch.equal(ids_a, ids_b) and torch.equal(c_a, c_b)
+    assert torch.equal(it, _T(init, "bf16")), "init_centroids was modified"
+    o_ids, o_c, o_n = O.kmeans(x, cfg.K, 50, 1e-2, init, "bf16")
+    assert abs(o_n - n_a) <= 1
+
+
+def test_verbose_path_equals_fused_loop(capsys):
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    cfg = synth.CONFIGS["c2"]
+    x, init = synth.make(cfg, N=8192)
+    xt, it = _T(x, "f16"), _T(init, "f16")
+    a = batch_kmeans_Euclid(xt, cfg.K, max_iters=4, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, cfg.K, max_iters=4, init_centroids=it, verbose=True)
+    assert "Iter 3, center shift" in capsys.readouterr().out
+    assert a[2] == b[2] == 4
+    assert torch.equal(a[0], b[0])
+    assert torch.equal(a[1], b[1])
+
+
+def test_deterministic_loop():
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    cfg = synth.CONFIGS["c3"]
+    x, init = synth.make(cfg, N=65536)
+    xt, it = _T(x, "f16"), _T(init, "f16")
+    a = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_c5_full_size_properties():
+    """Full mega config: invariants that do not need the oracle at full size."""
+    from flash_kmeans_cuda import _C, batch_kmeans_Euclid, synth
+    from flash_kmeans_cuda.ops import label_sort, row_sqnorm
+    cfg = synth.CONFIGS["c5"]
+    x, init = synth.make(cfg)
+    xt, it = _T(x, "f16"), _T(init, "f16")
+    ids, cents, n = batch_kmeans_Euclid(xt, cfg.K, max_iters=2, init_centroids=it)
+    assert n == 2 and ids.min() >= 0 and ids.max() < cfg.K
+    s, p = label_sort(ids, cfg.K)
+    assert torch.equal(torch.sort(p.long(), dim=1).values[0],
+                       torch.arange(cfg.N, device="cuda"))
+    assert bool((s[:, 1:] >= s[:, :-1]).all())
+    assert torch.equal(s.long(), torch.gather(ids.long(), 1, p.long()))
+    sums = torch.zeros((1, cfg.K, cfg.D), device="cuda")
+    cnt = torch.zeros((1, cfg.K), device="cuda", dtype=torch.int32)
+    _C.centroid_update_sorted_indexed(xt, p, s, sums, cnt)
+    assert int(cnt.sum()) == cfg.N
+    assert torch.equal(cnt[0].long(), torch.bincount(ids[0].long(), minlength=cfg.K))
+    tot = xt.float().sum(1)
+    assert torch.allclose(sums.sum(1), tot, rtol=1e-4, atol=1e-1)
+    # labels of a sampled subset against the oracle, with the GPU's centroids
+    rng = np.random.default_rng(0)
+    sub = rng.choice(cfg.N, 4096, replace=False)
+    c_np = _N(cents, "f16")
+    ids2 = _C.euclid_assign(xt, cents, row_sqnorm(xt), row_sqnorm(cents)).cpu().numpy()
+    ref = O.assign(x[:, sub], c_np, "f16")
+    nd, bad, worst = near_tie_report(x[:, sub], c_np, "f16", ids2[:, sub], ref)
+    assert bad == 0 and nd / sub.size < 2e-3

@@ -1,0 +1,162 @@
+"""GPU parity of label sort, centroid update and finalize (through the C ABI).
+
+Bar: the sort permutation and sorted labels are bit-exact against the
+oracle's stable sort; counts are bit-exact; fp32 sums agree with the
+oracle's float64 sums within fp32 accumulation error; finalize is bit-exact
+given identical sums and counts (IEEE division, round-to-nearest-even).
+Mirrors tests/cpp/smoke.cpp:55-95 of the reference (indexed update ==
+materialized update, finalize formula) plus skew, empty clusters, invalid
+labels and determinism.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kmeans_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dtype="i32"):
+    from flash_kmeans_cuda import synth
+    if dtype == "i32":
+        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+    return synth.to_torch(a, dtype)
+
+
+def _np(t, dtype=None):
+    from flash_kmeans_cuda import synth
+    torch.cuda.synchronize()
+    return t.cpu().numpy() if dtype is None else synth.from_torch(t, dtype)
+
+
+SORT_CASES = [
+    (1, 1, 1), (1, 100, 1), (2, 100, 2), (1, 4096, 255), (1, 4097, 256), (3, 10000, 257),
+    (1, 32768, 256), (1, 131072, 2048), (2, 65536, 1024), (1, 100000, 8192), (1, 70000, 70000),
+]
+
+
+@pytest.mark.parametrize("B,N,K", SORT_CASES)
+def test_label_sort_bit_exact(B, N, K):
+    from flash_kmeans_cuda.ops import label_sort
+    rng = np.random.default_rng(N + K)
+    ids = rng.integers(0, K, (B, N)).astype(np.int32)
+    if N > 50:
+        ids[:, rng.integers(0, N, N // 50)] = rng.integers(-3, 2 * K + 3, (B, N // 50))
+    s, p = label_sort(_t(ids), K)
+    es, ep = O.label_sort(ids, K)
+    assert np.array_equal(_np(p), ep)
+    assert np.array_equal(_np(s), es)
+
+
+def test_label_sort_zipf_skew():
+    from flash_kmeans_cuda.ops import label_sort
+    from flash_kmeans_cuda import synth
+    rng = np.random.default_rng(5)
+    ids = rng.choice(8192, 524288, p=synth.zipf_probs(8192, 1.1)).astype(np.int32)[None]
+    s, p = label_sort(_t(ids), 8192)
+    es, ep = O.label_sort(ids, 8192)
+    assert np.array_equal(_np(p), ep) and np.array_equal(_np(s), es)
+
+
+def _update_case(B, N, K, D, dtype, seed, invalid=False, zipf=False):
+    rng = np.random.default_rng(seed)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    if zipf:
+        from flash_kmeans_cuda import synth
+        ids = rng.choice(K, (B, N), p=synth.zipf_probs(K, 1.1)).astype(np.int32)
+    else:
+        ids = rng.integers(0, K, (B, N)).astype(np.int32)
+    if invalid:
+        ids[:, ::17] = -1
+        ids[:, 5::23] = K + 4
+    s_ids, perm = O.label_sort(ids, K)
+    return x, ids, s_ids, perm
+
+
+UPDATE_CASES = [
+    (1, 512, 16, 1, "f32"), (1, 512, 16, 7, "f32"), (1, 512, 16, 257, "f32"),
+    (1, 512, 64, 128, "f16"), (2, 5000, 300, 64, "bf16"), (1, 20000, 1000, 128, "f16"),
+    (1, 3000, 50, 600, "f16"), (1, 1000, 5, 1100, "bf16"), (3, 777, 1, 33, "f16"),
+]
+
+
+@pytest.mark.parametrize("B,N,K,D,dtype", UPDATE_CASES)
+def test_update_indexed_and_materialized(B, N, K, D, dtype):
+    from flash_kmeans_cuda import _C
+    x, ids, s_ids, perm = _update_case(B, N, K, D, dtype, seed=N + D, invalid=(D % 2 == 1))
+    xt = _t(x, dtype)
+    sums_i = torch.zeros((B, K, D), device="cuda")
+    cnt_i = torch.zeros((B, K), device="cuda", dtype=torch.int32)
+    _C.centroid_update_sorted_indexed(xt, _t(perm), _t(s_ids), sums_i, cnt_i)
+    rows = np.take_along_axis(x, perm.astype(np.int64)[..., None], 1)
+    sums_m = torch.zeros((B, K, D), device="cuda")
+    cnt_m = torch.zeros((B, K), device="cuda", dtype=torch.int32)
+    _C.centroid_update_sorted(_t(rows, dtype), _t(s_ids), sums_m, cnt_m)
+    es, ec = O.update_sorted_indexed(x, perm, s_ids, K, dtype)
+    si, ci, sm, cm = _np(sums_i), _np(cnt_i), _np(sums_m), _np(cnt_m)
+    assert np.array_equal(ci, ec) and np.array_equal(cm, ec)
+    # same rows in the same order -> bit-identical sums (smoke.cpp:81 asks 1e-4)
+    assert np.array_equal(si.view(np.uint32), sm.view(np.uint32))
+    tol = 1e-6 * np.maximum(ec[..., None], 1) * np.abs(O.to_f64(x, dtype)).max()
+    assert np.all(np.abs(si - es) <= tol + 1e-6 * np.abs(es))
+
+
+def test_update_zipf_skew_and_empty_clusters():
+    from flash_kmeans_cuda import _C
+    B, N, K, D = 1, 262144, 8192, 128
+    x, ids, s_ids, perm = _update_case(B, N, K, D, "f16", seed=9, zipf=True)
+    sums = torch.zeros((B, K, D), device="cuda")
+    cnt = torch.zeros((B, K), device="cuda", dtype=torch.int32)
+    _C.centroid_update_sorted_indexed(_t(x, "f16"), _t(perm), _t(s_ids), sums, cnt)
+    es, ec = O.update_sorted_indexed(x, perm, s_ids, K, "f16")
+    c = _np(cnt)
+    assert np.array_equal(c, ec) and (ec == 0).any() and ec.max() > 30000
+    s = _np(sums)
+    assert np.allclose(s, es, rtol=1e-5, atol=1e-5 * np.sqrt(np.maximum(ec, 1))[..., None])
+    assert np.all(s[ec == 0] == 0)
+
+
+def test_update_adds_into_existing_sums_and_is_deterministic():
+    from flash_kmeans_cuda import _C
+    x, ids, s_ids, perm = _update_case(2, 9000, 37, 64, "bf16", seed=4)
+    base = torch.full((2, 37, 64), 1.5, device="cuda")
+    basec = torch.full((2, 37), 3, device="cuda", dtype=torch.int32)
+    outs = []
+    for _ in range(2):
+        s, c = base.clone(), basec.clone()
+        _C.centroid_update_sorted_indexed(_t(x, "bf16"), _t(perm), _t(s_ids), s, c)
+        outs.append((_np(s), _np(c)))
+    es, ec = O.update_sorted_indexed(x, perm, s_ids, 37, "bf16")
+    assert np.array_equal(outs[0][1], ec + 3)
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32))
+    assert np.allclose(outs[0][0], es + 1.5, rtol=1e-5, atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("D", [1, 7, 64, 128, 257])
+def test_finalize_bit_exact(dtype, D):
+    from flash_kmeans_cuda import _C
+    rng = np.random.default_rng(D)
+    B, K = 2, 300
+    sums = (rng.standard_normal((B, K, D)) * 50).astype(np.float32)
+    counts = rng.integers(0, 9, (B, K)).astype(np.int32)
+    old = O.from_f32(rng.standard_normal((B, K, D)).astype(np.float32), dtype)
+    out = _C.centroid_finalize(_t(sums, "f32"), _t(counts), _t(old, dtype))
+    exp = O.finalize(sums, counts, old, dtype)
+    got = _np(out, dtype)
+    assert np.array_equal(np.asarray(got).view(np.uint8), np.asarray(exp).view(np.uint8))
+
+
+def test_finalize_in_place():
+    from flash_kmeans_cuda import _C
+    rng = np.random.default_rng(1)
+    sums = rng.standard_normal((1, 64, 32)).astype(np.float32)
+    counts = rng.integers(0, 3, (1, 64)).astype(np.int32)
+    old = O.from_f32(rng.standard_normal((1, 64, 32)).astype(np.float32), "f16")
+    t = _t(old, "f16")
+    _C.centroid_finalize(_t(sums, "f32"), _t(counts), t, out=t)
+    assert np.array_equal(_np(t, "f16"), O.finalize(sums, counts, old, "f16"))
