@@ -95,19 +95,24 @@ def build_torch_api() -> list[str]:
               "-I", INCLUDE, "-I", api_dir, "-I", os.path.join(ROCM, "include")]
     for i in incs:
         common += ["-isystem", i]
-    torch_libs = ["-L", tlib, "-Wl,-rpath," + tlib, "-ltorch", "-ltorch_cpu",
-                  "-ltorch_hip", "-lc10", "-lc10_hip", "-lamdhip64"]
+    # torch's libraries come first in DT_NEEDED so that torch's own HIP
+    # runtime (file libamdhip64.so, soname libamdhip64.so.7) is mapped before
+    # libfkc.so asks for libamdhip64.so.7: the loader then reuses it instead of
+    # mapping a second HIP runtime from /opt/rocm.  Nothing here links the HIP
+    # runtime directly.
+    torch_libs = ["-L", tlib, "-Wl,-rpath," + tlib, "-Wl,--no-as-needed",
+                  "-lc10_hip", "-ltorch_hip", "-lc10", "-ltorch_cpu", "-ltorch"]
     lib = os.path.join(PKG, "libflash_kmeans_cuda.so")
     _run([cxx, *common, "-shared", os.path.join(api_dir, "api.cpp"),
-          "-o", lib + ".tmp", "-L", PKG, "-Wl,-rpath,$ORIGIN", "-lfkc",
-          *torch_libs])
+          "-o", lib + ".tmp", *torch_libs, "-L", PKG, "-Wl,-rpath,$ORIGIN",
+          "-lfkc"])
     os.replace(lib + ".tmp", lib)
     bindir = os.path.join(PKG, "bin")
     os.makedirs(bindir, exist_ok=True)
     exe = os.path.join(bindir, "fkc_cpp_smoke")
     _run([cxx, *common, os.path.join(HERE, "cpp_tests", "smoke.cpp"),
-          "-o", exe + ".tmp", "-L", PKG, "-Wl,-rpath,$ORIGIN/..",
-          "-lflash_kmeans_cuda", "-lfkc", *torch_libs])
+          "-o", exe + ".tmp", *torch_libs, "-L", PKG,
+          "-Wl,-rpath,$ORIGIN/..", "-lflash_kmeans_cuda", "-lfkc"])
     os.replace(exe + ".tmp", exe)
     return [lib, exe]
 
