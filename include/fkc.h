@@ -99,7 +99,7 @@ FKC_CAPI int fkc_label_sort(const int32_t* cluster_ids, int32_t* sorted_ids,
 /*
  * Centroid accumulation over label-sorted rows.  Adds into sums/counts
  * (the caller zeroes them first, as _C.centroid_update_sorted expects,
- * bindings.cpp:65-79); labels outside [0,K) are skipped
+ * bindings.cpp:73-90); labels outside [0,K) are skipped
  * (update_sorted.cu:95,167).  ids_sorted must be non-decreasing over the
  * valid labels of each batch row.  Summation is fp32, in sorted order within
  * a run, and deterministic: the same inputs give the same bits.
