@@ -12,12 +12,13 @@
 //                  digit-major to hist[b][digit][tile];
 //   sort_scan    : exclusive scan of hist[b] (digit-major, so the scan gives
 //                  every (digit, tile) its global output offset);
-//   sort_scatter : each wave ranks its 1024 keys (16 chunks of 64) stably:
-//                  a ballot per digit bit yields, for every lane, the mask of
-//                  lanes holding the same digit ("multi-split"); its rank is
-//                  the per-wave digit counter plus the matching lanes below
-//                  it.  Per-wave counters are then prefix-summed across the
-//                  4 waves and offset by the tile's scanned base.
+//   sort_scatter : each of 8 waves ranks its 512 keys (8 chunks of 64)
+//                  stably: a ballot per digit bit yields, for every lane, the
+//                  mask of lanes holding the same digit ("multi-split"); its
+//                  rank is the per-wave digit counter plus the matching lanes
+//                  below it.  Keys are placed in LDS in tile-sorted order,
+//                  then each digit's run is copied to its global slot, so the
+//                  writes are runs of consecutive addresses.
 // The carried payload is the original index; the last pass writes the
 // user's sorted_ids / perm.
 #include "device_util.hpp"
@@ -26,9 +27,10 @@
 namespace fkc {
 namespace {
 
-constexpr int ST = 256;           // threads per workgroup
-constexpr int SW = ST / 64;       // waves
-constexpr int TILE = 4096;        // keys per workgroup
+constexpr int TILE = 4096;        // keys per tile (one workgroup)
+constexpr int HT = 256;           // threads of the histogram kernel
+constexpr int ST = 512;           // threads of the scatter kernel
+constexpr int SW = ST / 64;       // scatter waves
 constexpr int PER_WAVE = TILE / SW;
 constexpr int CHUNKS = PER_WAVE / 64;
 
@@ -36,9 +38,13 @@ __device__ inline uint32_t sort_key(int32_t id, int K) {
   return (uint32_t)id < (uint32_t)K ? (uint32_t)id : (uint32_t)K;
 }
 
-__global__ void __launch_bounds__(ST)
+// Per-batch stride of the digit table: room for 256 digits x ntiles,
+// rounded to whole int4s so every batch row starts 16-byte aligned.
+inline int64_t table_stride(int64_t ntiles) { return (256 * ntiles + 3) / 4 * 4; }
+
+__global__ void __launch_bounds__(HT)
 sort_hist_kernel(const int32_t* __restrict__ keys, int32_t* __restrict__ hist,
-                 int N, int K, int shift, int bits, int ntiles,
+                 int N, int K, int shift, int bits, int ntiles, int64_t hstride,
                  const int32_t* __restrict__ ctrl) {
   if (loop_done(ctrl)) return;
   __shared__ int h[256];
@@ -49,32 +55,35 @@ sort_hist_kernel(const int32_t* __restrict__ keys, int32_t* __restrict__ hist,
   __syncthreads();
   const int32_t* kb = keys + (size_t)b * N;
   const int base = tile * TILE;
-  for (int i = tid; i < TILE; i += ST) {
+  const uint32_t dmask = (uint32_t)(nb - 1);
+  for (int i = tid; i < TILE; i += HT) {
     const int n = base + i;
-    if (n < N) {
-      const uint32_t d = (sort_key(kb[n], K) >> shift) & (uint32_t)(nb - 1);
-      atomicAdd(&h[d], 1);
-    }
+    if (n < N) atomicAdd(&h[(sort_key(kb[n], K) >> shift) & dmask], 1);
   }
   __syncthreads();
-  if (tid < nb) hist[((size_t)b * nb + tid) * ntiles + tile] = h[tid];
+  if (tid < nb) hist[(size_t)b * hstride + (size_t)tid * ntiles + tile] = h[tid];
 }
 
-// In-place exclusive scan of one batch row of the histogram table
-// (len = bins * ntiles entries).  One 1024-thread workgroup per batch row.
+// In-place exclusive scan of one batch row of the digit table (len = bins x
+// ntiles entries, digit-major).  One 1024-thread workgroup per batch row;
+// each thread owns a contiguous, 4-aligned segment read with 16-byte loads.
 __global__ void __launch_bounds__(1024)
-sort_scan_kernel(int32_t* __restrict__ hist, int64_t len,
+sort_scan_kernel(int32_t* __restrict__ hist, int64_t len, int64_t hstride,
                  const int32_t* __restrict__ ctrl) {
   if (loop_done(ctrl)) return;
   __shared__ int wsum[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int32_t* hb = hist + (size_t)blockIdx.x * len;
-  const int64_t per = (len + 1023) / 1024;
-  const int64_t lo = tid * per;
-  const int64_t hi = lo + per < len ? lo + per : len;
+  int32_t* hb = hist + (size_t)blockIdx.x * hstride;
+  const int64_t per = ((len + 1023) / 1024 + 3) / 4 * 4;
+  const int64_t lo = min((int64_t)tid * per, len);
+  const int64_t hi = min(lo + per, len);
   int local = 0;
-  for (int64_t i = lo; i < hi; ++i) local += hb[i];
-  // Inclusive scan across the wave, then across waves.
+  int64_t i = lo;
+  for (; i + 4 <= hi; i += 4) {
+    const int4 v = *reinterpret_cast<const int4*>(hb + i);
+    local += v.x + v.y + v.z + v.w;
+  }
+  for (; i < hi; ++i) local += hb[i];
   int incl = local;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -83,43 +92,65 @@ sort_scan_kernel(int32_t* __restrict__ hist, int64_t len,
   }
   if (lane == 63) wsum[wave] = incl;
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < 16; ++w) {
-      const int v = wsum[w];
-      wsum[w] = run;
-      run += v;
+  if (tid < 64) {
+    int v = tid < 16 ? wsum[tid] : 0;
+    int inc = v;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const int u = __shfl_up(inc, off, 64);
+      if (tid >= off) inc += u;
     }
+    if (tid < 16) wsum[tid] = inc - v;
   }
   __syncthreads();
   int run = wsum[wave] + incl - local;  // exclusive prefix of this thread
-  for (int64_t i = lo; i < hi; ++i) {
+  i = lo;
+  for (; i + 4 <= hi; i += 4) {
+    int4 v = *reinterpret_cast<const int4*>(hb + i);
+    int4 o;
+    o.x = run; run += v.x;
+    o.y = run; run += v.y;
+    o.z = run; run += v.z;
+    o.w = run; run += v.w;
+    *reinterpret_cast<int4*>(hb + i) = o;
+  }
+  for (; i < hi; ++i) {
     const int v = hb[i];
     hb[i] = run;
     run += v;
   }
 }
 
+// Stable rank of every key of one tile by its digit, then a coalesced
+// write-out: keys are first placed in LDS in tile-sorted order, then each
+// digit's contiguous run is copied to its global slot.
 __global__ void __launch_bounds__(ST)
 sort_scatter_kernel(const int32_t* __restrict__ keys_in,
                     const int32_t* __restrict__ vals_in,
                     int32_t* __restrict__ keys_out,
                     int32_t* __restrict__ vals_out,
                     const int32_t* __restrict__ offs, int N, int K, int shift,
-                    int bits, int ntiles, const int32_t* __restrict__ ctrl) {
+                    int bits, int ntiles, int64_t hstride,
+                    const int32_t* __restrict__ ctrl) {
   if (loop_done(ctrl)) return;
   __shared__ int cnt[SW][256];
-  __shared__ int toff[256];
+  __shared__ int dstart[256];
+  __shared__ int gbase[256];
+  __shared__ int wtot[4];
+  __shared__ int32_t skey[TILE];
+  __shared__ int32_t sval[TILE];
   const int nb = 1 << bits;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tile = blockIdx.x, b = blockIdx.y;
   for (int i = tid; i < SW * 256; i += ST) (&cnt[0][0])[i] = 0;
-  if (tid < nb) toff[tid] = offs[((size_t)b * nb + tid) * ntiles + tile];
+  if (tid < nb) gbase[tid] = offs[(size_t)b * hstride + (size_t)tid * ntiles + tile];
   __syncthreads();
 
   const int32_t* kb = keys_in + (size_t)b * N;
   const int32_t* vb = vals_in ? vals_in + (size_t)b * N : nullptr;
-  const int base = tile * TILE + wave * PER_WAVE;
+  const int tbase = tile * TILE;
+  const int tn = min(TILE, N - tbase);  // keys in this tile
+  const int base = tbase + wave * PER_WAVE;
   int32_t kk[CHUNKS], vv[CHUNKS];
   int rank[CHUNKS], dig[CHUNKS];
   const uint32_t dmask = (uint32_t)(nb - 1);
@@ -145,24 +176,50 @@ sort_scatter_kernel(const int32_t* __restrict__ keys_in,
     dig[c] = (int)d;
   }
   __syncthreads();
-  if (tid < nb) {
-    int run = toff[tid];
-    for (int w = 0; w < SW; ++w) {
-      const int v = cnt[w][tid];
-      cnt[w][tid] = run;
-      run += v;
+  // per digit: offsets of each wave inside the digit, and the digit total
+  int total = 0;
+  if (tid < 256) {
+    if (tid < nb) {
+      for (int w = 0; w < SW; ++w) {
+        const int v = cnt[w][tid];
+        cnt[w][tid] = total;
+        total += v;
+      }
+    }
+    // exclusive scan of digit totals over the 256 digits (waves 0..3)
+    int incl = total;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int u = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += u;
+    }
+    if (lane == 63) wtot[wave] = incl;
+    dstart[tid] = incl - total;  // within-wave exclusive prefix for now
+  }
+  __syncthreads();
+  if (tid < 256) {
+    int add = 0;
+    for (int w = 0; w < wave; ++w) add += wtot[w];
+    dstart[tid] += add;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    if (rank[c] >= 0) {
+      const int pos = dstart[dig[c]] + cnt[wave][dig[c]] + rank[c];
+      skey[pos] = kk[c];
+      sval[pos] = vv[c];
     }
   }
   __syncthreads();
   int32_t* ko = keys_out + (size_t)b * N;
   int32_t* vo = vals_out + (size_t)b * N;
-#pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    if (rank[c] >= 0) {
-      const int pos = cnt[wave][dig[c]] + rank[c];
-      ko[pos] = kk[c];
-      vo[pos] = vv[c];
-    }
+  for (int i = tid; i < tn; i += ST) {
+    const int32_t key = skey[i];
+    const int d = (int)((sort_key(key, K) >> shift) & dmask);
+    const int pos = gbase[d] + (i - dstart[d]);
+    ko[pos] = key;
+    vo[pos] = sval[i];
   }
 }
 
@@ -189,7 +246,7 @@ SortPlan sort_plan(int64_t N, int64_t K, bool labels_valid) {
 size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K) {
   const SortPlan p = sort_plan(N, K, false);  // the larger of the two plans
   Carve c(nullptr);
-  c.take<int32_t>((size_t)B * 256 * (size_t)p.ntiles);  // histogram table
+  c.take<int32_t>((size_t)B * table_stride(p.ntiles));  // digit table
   const int tmp = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
   for (int i = 0; i < tmp; ++i) {
     c.take<int32_t>((size_t)B * N);  // keys
@@ -209,7 +266,8 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
                 ws_bytes, need);
   const SortPlan p = sort_plan(N, K, labels_valid);
   Carve c(ws);
-  int32_t* hist = c.take<int32_t>((size_t)B * 256 * (size_t)p.ntiles);
+  const int64_t hstride = table_stride(p.ntiles);
+  int32_t* hist = c.take<int32_t>((size_t)B * hstride);
   int32_t* tk[2] = {nullptr, nullptr};
   int32_t* tv[2] = {nullptr, nullptr};
   const int tmp = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
@@ -229,18 +287,18 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
     int32_t* vout = last ? perm : tv[i % 2];
     const int nb = 1 << p.bits[i];
     dim3 grid((unsigned)p.ntiles, (unsigned)B);
-    hipLaunchKernelGGL(sort_hist_kernel, grid, dim3(ST), 0, s, kin, hist,
+    hipLaunchKernelGGL(sort_hist_kernel, grid, dim3(HT), 0, s, kin, hist,
                        (int)N, (int)K, p.shift[i], p.bits[i], (int)p.ntiles,
-                       ctrl);
+                       hstride, ctrl);
     int rc = check_launch("sort_hist");
     if (rc) return rc;
     hipLaunchKernelGGL(sort_scan_kernel, dim3((unsigned)B), dim3(1024), 0, s,
-                       hist, (int64_t)nb * p.ntiles, ctrl);
+                       hist, (int64_t)nb * p.ntiles, hstride, ctrl);
     rc = check_launch("sort_scan");
     if (rc) return rc;
     hipLaunchKernelGGL(sort_scatter_kernel, grid, dim3(ST), 0, s, kin, vin,
                        kout, vout, hist, (int)N, (int)K, p.shift[i],
-                       p.bits[i], (int)p.ntiles, ctrl);
+                       p.bits[i], (int)p.ntiles, hstride, ctrl);
     rc = check_launch("sort_scatter");
     if (rc) return rc;
     kin = kout;

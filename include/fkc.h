@@ -62,7 +62,7 @@ FKC_CAPI const char* fkc_version(void);
  * the lowest k winning exact ties.
  * Replaces fkc::euclid_assign_out (flash_kmeans_cuda.h:41-46, api.cpp:58-72)
  * and _C.euclid_assign (bindings.cpp:43-63).
- *   - fp16/bf16 with D % 16 == 0 and D <= 256: MFMA kernel ranking
+ *   - fp16/bf16 with D % 8 == 0 and D <= 512: MFMA kernel ranking
  *     c_sq[k] - 2<x,c_k> in fp32 (x_sq is not read; like the reference's
  *     raw-distance route, assign_sm80.cu:437-441, 687).
  *   - every other case, and FKC_ASSIGN_FORCE_SAFE=1: fp32 VALU kernel ranking

@@ -66,8 +66,10 @@ def test_mfma_assign_matches_oracle(dtype, B, N, K, D):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("D", [16 * s for s in range(1, 17)])
+@pytest.mark.parametrize("D", [16 * s for s in range(1, 17)] + [8, 24, 40, 72, 264, 384, 448, 512])
 def test_mfma_every_feature_width(dtype, D):
+    """Every 32-feature step count (D <= 512, D % 8 == 0; widths that are not
+    a multiple of 32 are zero-padded inside the kernel)."""
     x, c = _data(1, 300, 97, D, dtype, seed=D)
     _check(x, c, dtype, _gpu_assign(x, c, dtype))
 
@@ -131,9 +133,9 @@ def test_fp32_route_matches_oracle(B, N, K, D):
     _check(x, c, "f32", got, max_frac=1e-3 if B * N >= 4096 else None)
 
 
-@pytest.mark.parametrize("D", [1, 7, 31, 48, 257, 300])
+@pytest.mark.parametrize("D", [1, 7, 31, 48, 257, 300, 520])
 def test_fp16_odd_widths_use_fp32_route(D):
-    """D % 16 != 0 or D > 256 fall back to the fp32 kernel (smoke.cpp:104)."""
+    """D % 8 != 0 or D > 512 take the fp32 kernel (widths from smoke.cpp:104)."""
     x, c = _data(1, 512, 64, D, "f16", seed=D)
     got = _gpu_assign(x, c, "f16")
     _check(x, c, "f16", got)
