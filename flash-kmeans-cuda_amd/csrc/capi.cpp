@@ -273,6 +273,9 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
   if (!workspace || workspace_bytes < need)
     return fail(FKC_ERR_WORKSPACE, "kmeans_lloyd: workspace %zu < %zu bytes",
                 workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) % kWorkspaceAlign != 0)
+    return fail(FKC_ERR_WORKSPACE, "kmeans_lloyd: workspace not %d-byte aligned",
+                kWorkspaceAlign);
   LoopBuffers L = carve_loop(workspace, B, N, K, D, dtype, max_iters, nullptr);
 
   const bool check = tol > 0.f;

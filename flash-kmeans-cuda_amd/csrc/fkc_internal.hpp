@@ -20,6 +20,11 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline size_t dtype_size(int dtype) { return dtype == FKC_F32 ? 4 : 2; }
 
 // Bump allocator over a caller-owned workspace.
+// Workspaces are carved in 256-byte aligned slices and read with 16-byte
+// vector loads, so their base must be 256-byte aligned (hipMalloc and the
+// torch caching allocator return such pointers).
+constexpr int kWorkspaceAlign = 256;
+
 struct Carve {
   char* base;
   size_t used = 0;
@@ -33,7 +38,7 @@ struct Carve {
 };
 
 // ---------------------------------------------------------------- assign
-// Routing predicate: the MFMA kernel serves fp16/bf16, D % 16 == 0, D <= 256.
+// Routing predicate: the MFMA kernel serves fp16/bf16, D % 8 == 0, D <= 512.
 bool assign_uses_mfma(int dtype, int64_t D);
 int launch_assign(const void* x, const void* c, const float* x_sq,
                   const float* c_sq, int32_t* ids, int64_t B, int64_t N,

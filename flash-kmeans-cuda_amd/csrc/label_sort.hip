@@ -264,6 +264,9 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
   if (ws_bytes < need || (need > 0 && ws == nullptr))
     return fail(FKC_ERR_WORKSPACE, "label_sort: workspace %zu < %zu bytes",
                 ws_bytes, need);
+  if (reinterpret_cast<uintptr_t>(ws) % kWorkspaceAlign != 0)
+    return fail(FKC_ERR_WORKSPACE, "label_sort: workspace not %d-byte aligned",
+                kWorkspaceAlign);
   const SortPlan p = sort_plan(N, K, labels_valid);
   Carve c(ws);
   const int64_t hstride = table_stride(p.ntiles);

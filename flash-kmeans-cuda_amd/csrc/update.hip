@@ -12,15 +12,25 @@
 //   update_runs  : one wave per unit of 128 consecutive sorted rows.  Lanes
 //                  own column slices (64 lanes x VEC x NI columns per pass
 //                  over the row), so every row is one coalesced load per
-//                  lane slice; rows are fetched eight at a time (through the
-//                  permutation for the indexed variant) before being folded
-//                  into the run accumulator.  A run wholly inside the unit is
+//                  lane slice; a unit's labels and permutation entries are
+//                  loaded up front, then rows are fetched 32 / NI at a time
+//                  (through the permutation for the indexed variant) before
+//                  being folded into the run accumulator.  A run wholly inside the unit is
 //                  written directly.  A run entering from the previous unit
 //                  ("head") or leaving into the next ("tail") is parked in a
 //                  per-unit partial slot instead.
-//   update_merge : the unit where a multi-unit run starts owns it: it adds
-//                  its tail partial to the heads of the following units, in
-//                  unit order, and writes the bin once.
+//   update_blocks: a run can span many units (few clusters, many points).
+//                  For every block of 64 units that lies wholly inside one
+//                  run, one wave adds the block's 64 head partials in unit
+//                  order into a block partial.
+//   update_merge : the unit where a multi-unit run starts owns it.  It finds
+//                  the run's last unit by ballots over unit and block flags,
+//                  then adds, in unit order, its tail partial, the heads of
+//                  the following units in its own block, the partials of the
+//                  blocks the run covers, and the heads of the units of the
+//                  block where the run ends; the bin is written once.  A run
+//                  over L units adds at most 127 + L/64 partial rows, 32 rows
+//                  in flight per wave (four lane groups, eight rows each).
 //
 // Mode "add" (the _C / C-ABI contract) adds into caller-zeroed outputs;
 // mode "overwrite" (the Lloyd loop, where every label is valid) stores, and
@@ -31,32 +41,51 @@
 
 #include <limits.h>
 
+#include <type_traits>
+
 namespace fkc {
 namespace {
 
 constexpr int UR = 128;  // sorted rows per unit (one wave)
 constexpr int UT = 256;  // threads per workgroup: 4 units
+constexpr int UB = 64;   // units per block of the two-level run merge
 
-// VEC consecutive columns of one row as fp32 (VEC in {1, 2}).
+// VEC consecutive columns of one row as one raw load (VEC in {1, 2}), and
+// their conversion to fp32.
 template <int DT, int VEC>
-__device__ inline void load_cols(const typename Elem<DT>::T* p, float* out) {
-  using E = Elem<DT>;
-  if constexpr (VEC == 1) {
-    out[0] = E::load(p[0]);
-  } else if constexpr (DT == FKC_F32) {
-    const float2 v = *reinterpret_cast<const float2*>(p);
-    out[0] = v.x;
-    out[1] = v.y;
-  } else {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-    typename E::T lo, hi;
-    const uint16_t l16 = (uint16_t)(w & 0xffffu), h16 = (uint16_t)(w >> 16);
-    __builtin_memcpy(&lo, &l16, 2);
-    __builtin_memcpy(&hi, &h16, 2);
-    out[0] = E::load(lo);
-    out[1] = E::load(hi);
+struct RawCols;
+template <int VEC>
+struct RawCols<FKC_F32, VEC> {
+  using T = typename std::conditional<VEC == 2, float2, float>::type;
+  __device__ static T load(const float* p) { return *reinterpret_cast<const T*>(p); }
+  __device__ static T zero() { return T{}; }
+  __device__ static void cvt(T r, float* out) {
+    if constexpr (VEC == 2) {
+      out[0] = r.x;
+      out[1] = r.y;
+    } else {
+      out[0] = r;
+    }
   }
-}
+};
+template <int DT, int VEC>
+struct RawCols {  // 16-bit element types
+  using E = Elem<DT>;
+  using T = typename std::conditional<VEC == 2, uint32_t, uint16_t>::type;
+  __device__ static T load(const typename E::T* p) {
+    return *reinterpret_cast<const T*>(p);
+  }
+  __device__ static T zero() { return 0; }
+  __device__ static void cvt(T r, float* out) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const uint16_t h = (uint16_t)((uint32_t)r >> (16 * v));
+      typename E::T e;
+      __builtin_memcpy(&e, &h, 2);
+      out[v] = E::load(e);
+    }
+  }
+};
 
 struct UnitMeta {  // per unit, int32 x 4
   enum { TAIL_ID = 0, TAIL_LEN = 1, HEAD_LEN = 2, THROUGH = 3 };
@@ -72,6 +101,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
                    int nunits, int overwrite,
                    const int32_t* __restrict__ ctrl) {
   using T = typename Elem<DT>::T;
+  constexpr int RB = 32 / NI;  // rows in flight per wave
   if (loop_done(ctrl)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.y;
@@ -169,39 +199,47 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     }
   };
 
-  int cur = ib[p0];
+  // Labels and permutation entries of the unit's rows, one per lane per
+  // 64-row chunk, loaded up front.
+  constexpr int CH = UR / 64;
+  int ivs[CH], pvs[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int p = p0 + c * 64 + lane;
+    ivs[c] = p < p1 ? ib[p] : 0;
+    pvs[c] = INDEXED ? (p < p1 ? pb[p] : 0) : p;
+  }
+
+  int cur = __builtin_amdgcn_readfirstlane(ivs[0]);
   int rs = p0;
   if (overwrite && !(has_prev && prev == cur))
     zero_bins(has_prev ? prev + 1 : 0, cur);
 
-  for (int base = p0; base < p1; base += 64) {
+  using R = typename RawCols<DT, VEC>::T;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int base = p0 + c * 64;
+    if (base >= p1) break;
     const int nrow = min(64, p1 - base);
-    const int iv = lane < nrow ? ib[base + lane] : 0;
-    const int pv = INDEXED ? (lane < nrow ? pb[base + lane] : 0) : base + lane;
-    for (int j0 = 0; j0 < nrow; j0 += 8) {
-      float val[8][NI][VEC];
+    const int iv = ivs[c], pv = pvs[c];
+    for (int j0 = 0; j0 < nrow; j0 += RB) {
+      // RB rows in flight: raw column words first, conversion when folded.
+      R raw[RB][NI];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
+      for (int jj = 0; jj < RB; ++jj) {
         const int j = j0 + jj;
-        if (j < nrow) {
-          const int row = __builtin_amdgcn_readlane(pv, j);
-          // A permutation entry outside [0,N) contributes zeros instead of
-          // reading outside x.
-          const bool rok = (uint32_t)row < (uint32_t)N;
-          const T* xr = xb + (size_t)(rok ? row : 0) * D;
+        const int row = __builtin_amdgcn_readlane(pv, j < nrow ? j : 0);
+        // A permutation entry outside [0,N), or a row past the unit, reads
+        // nothing and contributes zeros.
+        const bool rok = j < nrow && (uint32_t)row < (uint32_t)N;
+        const T* xr = xb + (size_t)(rok ? row : 0) * D;
 #pragma unroll
-          for (int i = 0; i < NI; ++i) {
-            if (cok[i] && rok) {
-              load_cols<DT, VEC>(xr + col[i], val[jj][i]);
-            } else {
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) val[jj][i][v] = 0.f;
-            }
-          }
-        }
+        for (int i = 0; i < NI; ++i)
+          raw[jj][i] = (cok[i] && rok) ? RawCols<DT, VEC>::load(xr + col[i])
+                                       : RawCols<DT, VEC>::zero();
       }
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
+      for (int jj = 0; jj < RB; ++jj) {
         const int j = j0 + jj;
         if (j < nrow) {
           const int id = __builtin_amdgcn_readlane(iv, j);
@@ -216,9 +254,12 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
               for (int v = 0; v < VEC; ++v) acc[i][v] = 0.f;
           }
 #pragma unroll
-          for (int i = 0; i < NI; ++i)
+          for (int i = 0; i < NI; ++i) {
+            float f[VEC];
+            RawCols<DT, VEC>::cvt(raw[jj][i], f);
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) acc[i][v] += val[jj][i][v];
+            for (int v = 0; v < VEC; ++v) acc[i][v] += f[v];
+          }
         }
       }
     }
@@ -235,12 +276,120 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   }
 }
 
-// One wave per unit; only units holding a tail partial do work.
+// Wave-cooperative ordered sum of partial rows (D fp32 each):
+//   out[c] = first[c] + row(0)[c] + ... + row(n-1)[c]   (first may be null)
+// The wave splits into G lane groups; group g sums rows i = g, g+G, g+2G ...
+// in increasing i (eight loads in flight per lane before their adds) over
+// V-wide column vectors, then the group sums are added in group order.  The
+// bracketing depends only on n, so the result is reproducible bit for bit.
+// Mode 0 stores out, mode 1 adds into it.
+template <int V>
+__device__ inline void ld_cols(const float* p, float* o) {
+  if constexpr (V == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else {
+    o[0] = p[0];
+  }
+}
+
+template <int V, typename RowFn>
+__device__ inline void wave_ordered_sum(const float* first, int n, int D,
+                                        RowFn row, float* out, int add,
+                                        int lane) {
+  constexpr int G = 4, LG = 64 / G, PF = 8;
+  const int g = lane / LG, sub = lane % LG;
+  for (int c0 = 0; c0 < D; c0 += LG * V) {
+    const int c = c0 + sub * V;
+    const bool cok = c < D;  // D % V == 0: the whole vector is in range
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.f;
+    if (first != nullptr && g == 0 && cok) ld_cols<V>(first + c, acc);
+    for (int i0 = g; i0 < n; i0 += G * PF) {
+      float t[PF][V];
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        const int i = i0 + j * G;
+        if (cok && i < n) {
+          ld_cols<V>(row(i) + c, t[j]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v) t[j][v] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < PF; ++j)
+        if (i0 + j * G < n) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[v] += t[j][v];
+        }
+    }
+    float tot[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) tot[v] = __shfl(acc[v], sub, 64);
+#pragma unroll
+    for (int gg = 1; gg < G; ++gg)
+#pragma unroll
+      for (int v = 0; v < V; ++v) tot[v] += __shfl(acc[v], gg * LG + sub, 64);
+    if (g == 0 && cok) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) out[c + v] = add ? out[c + v] + tot[v] : tot[v];
+    }
+  }
+}
+
+// One wave per block of UB units.  A block whose every unit lies inside a
+// single run ("full") gets the ordered sum of its head partials and its row
+// count; other blocks are flagged not full.
+__global__ void __launch_bounds__(UT)
+update_blocks_kernel(const float* __restrict__ part,
+                     const int32_t* __restrict__ meta,
+                     float* __restrict__ bpart, int32_t* __restrict__ bmeta,
+                     int D, int nunits, int nblocks,
+                     const int32_t* __restrict__ ctrl) {
+  if (loop_done(ctrl)) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.y;
+  const int beta = blockIdx.x * (UT / 64) + wave;
+  if (beta >= nblocks) return;
+  const int32_t* mb = meta + (size_t)b * nunits * 4;
+  const int v = beta * UB + lane;
+  const bool thr = v < nunits && mb[(size_t)v * 4 + UnitMeta::THROUGH] != 0;
+  const int hl = v < nunits ? mb[(size_t)v * 4 + UnitMeta::HEAD_LEN] : 0;
+  const bool full = __builtin_amdgcn_ballot_w64(thr) == ~0ull;
+  int32_t* bm = bmeta + ((size_t)b * nblocks + beta) * 2;
+  const int len = wave_sum_i(hl);
+  if (!full) {
+    if (lane == 0) {
+      bm[0] = 0;
+      bm[1] = 0;
+    }
+    return;
+  }
+  const float* pb = part + (size_t)b * nunits * 2 * D;
+  float* dst = bpart + ((size_t)b * nblocks + beta) * D;
+  const int v0 = beta * UB;
+  auto row = [&](int i) { return pb + ((size_t)(v0 + i) * 2 + 0) * D; };
+  if (D % 4 == 0)
+    wave_ordered_sum<4>(nullptr, UB, D, row, dst, 0, lane);
+  else
+    wave_ordered_sum<1>(nullptr, UB, D, row, dst, 0, lane);
+  if (lane == 0) {
+    bm[0] = 1;
+    bm[1] = len;
+  }
+}
+
+// One wave per unit; only units holding a tail partial (run owners) work.
 __global__ void __launch_bounds__(UT)
 update_merge_kernel(const float* __restrict__ part,
-                    const int32_t* __restrict__ meta, float* __restrict__ sums,
+                    const int32_t* __restrict__ meta,
+                    const float* __restrict__ bpart,
+                    const int32_t* __restrict__ bmeta, float* __restrict__ sums,
                     int32_t* __restrict__ counts, int K, int D, int nunits,
-                    int overwrite, const int32_t* __restrict__ ctrl) {
+                    int nblocks, int overwrite,
+                    const int32_t* __restrict__ ctrl) {
   if (loop_done(ctrl)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.y;
@@ -251,28 +400,65 @@ update_merge_kernel(const float* __restrict__ part,
   if (tail_len == 0) return;
   const int id = mb[(size_t)u * 4 + UnitMeta::TAIL_ID];
   if ((uint32_t)id >= (uint32_t)K) return;
-  const float* pb = part + (size_t)b * nunits * 2 * D;
-  float* dst = sums + ((size_t)b * K + id) * D;
-  int len = tail_len;
-  for (int c0 = 0; c0 < D; c0 += 64) {
-    const int c = c0 + lane;
-    float acc = c < D ? pb[((size_t)u * 2 + 1) * D + c] : 0.f;
-    int v = u + 1;
-    int l = tail_len;
-    while (v < nunits) {
-      if (c < D) acc += pb[((size_t)v * 2 + 0) * D + c];
-      l += mb[(size_t)v * 4 + UnitMeta::HEAD_LEN];
-      if (!mb[(size_t)v * 4 + UnitMeta::THROUGH]) break;
-      ++v;
-    }
-    len = l;
-    if (c < D) {
-      if (overwrite)
-        dst[c] = acc;
-      else
-        dst[c] += acc;
+  const int32_t* bmb = bmeta + (size_t)b * nblocks * 2;
+
+  // The run continues through units u+1 .. e (e = first unit after u that
+  // is not wholly inside the run; the last unit never is, so e exists).
+  // Items, in order: heads of units u+1 .. min(e, end of u's block), then
+  // full blocks, then heads of the units of the block holding e.
+  const int bend = min((u / UB + 1) * UB, nunits);
+  int n1, nblk = 0, n3 = 0, beta0 = u / UB + 1, v3 = 0;
+  {
+    const int v = u + 1 + lane;
+    const bool stop =
+        v < bend && mb[(size_t)v * 4 + UnitMeta::THROUGH] == 0;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(stop);
+    if (m) {
+      n1 = __builtin_ctzll(m) + 1;  // units u+1 .. u+n1
+    } else {
+      n1 = bend - (u + 1);
+      int be = -1;
+      for (int b0 = beta0; be < 0 && b0 < nblocks; b0 += 64) {
+        const int bb = b0 + lane;
+        const bool nf = bb < nblocks && bmb[(size_t)bb * 2] == 0;
+        const uint64_t mm = __builtin_amdgcn_ballot_w64(nf);
+        if (mm) be = b0 + (int)__builtin_ctzll(mm);
+      }
+      if (be < 0) be = nblocks - 1;  // unreachable: the last block is not full
+      nblk = be - beta0;
+      v3 = be * UB;
+      const int w = v3 + lane;
+      const bool st = w < nunits && mb[(size_t)w * 4 + UnitMeta::THROUGH] == 0;
+      const uint64_t m3 = __builtin_amdgcn_ballot_w64(st);
+      n3 = m3 ? (int)__builtin_ctzll(m3) + 1 : min(UB, nunits - v3);
     }
   }
+  const int n = n1 + nblk + n3;
+  const float* pb = part + (size_t)b * nunits * 2 * D;
+  const float* bp = bpart + (size_t)b * nblocks * D;
+  auto row = [&](int i) -> const float* {
+    if (i < n1) return pb + ((size_t)(u + 1 + i) * 2 + 0) * D;
+    if (i < n1 + nblk) return bp + (size_t)(beta0 + i - n1) * D;
+    return pb + ((size_t)(v3 + i - n1 - nblk) * 2 + 0) * D;
+  };
+  // Row count: lanes over items, then a wave sum (integer, order-free).
+  int l = 0;
+  for (int i = lane; i < n; i += 64) {
+    if (i < n1)
+      l += mb[(size_t)(u + 1 + i) * 4 + UnitMeta::HEAD_LEN];
+    else if (i < n1 + nblk)
+      l += bmb[(size_t)(beta0 + i - n1) * 2 + 1];
+    else
+      l += mb[(size_t)(v3 + i - n1 - nblk) * 4 + UnitMeta::HEAD_LEN];
+  }
+  const int len = tail_len + wave_sum_i(l);
+
+  float* dst = sums + ((size_t)b * K + id) * D;
+  const float* tail = pb + ((size_t)u * 2 + 1) * D;
+  if (D % 4 == 0)
+    wave_ordered_sum<4>(tail, n, D, row, dst, overwrite ? 0 : 1, lane);
+  else
+    wave_ordered_sum<1>(tail, n, D, row, dst, overwrite ? 0 : 1, lane);
   if (lane == 0) {
     int32_t* cp = counts + (size_t)b * K + id;
     if (overwrite)
@@ -324,9 +510,12 @@ int launch_runs_dt(const void* x, const int32_t* perm, const int32_t* sids,
 
 size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D) {
   const int64_t nunits = (N + UR - 1) / UR;
+  const int64_t nblocks = (nunits + UB - 1) / UB;
   Carve c(nullptr);
-  c.take<float>((size_t)B * nunits * 2 * D);
-  c.take<int32_t>((size_t)B * nunits * 4);
+  c.take<float>((size_t)B * nunits * 2 * D);     // unit head/tail partials
+  c.take<int32_t>((size_t)B * nunits * 4);       // unit metadata
+  c.take<float>((size_t)B * nblocks * D);        // block partials
+  c.take<int32_t>((size_t)B * nblocks * 2);      // block flag, row count
   return c.used;
 }
 
@@ -345,10 +534,17 @@ int launch_update(const void* x, const int32_t* perm,
   if (ws_bytes < need || ws == nullptr)
     return fail(FKC_ERR_WORKSPACE, "centroid_update: workspace %zu < %zu bytes",
                 ws_bytes, need);
+  if (reinterpret_cast<uintptr_t>(ws) % kWorkspaceAlign != 0)
+    return fail(FKC_ERR_WORKSPACE,
+                "centroid_update: workspace not %d-byte aligned",
+                kWorkspaceAlign);
   const int64_t nunits = (N + UR - 1) / UR;
   Carve c(ws);
+  const int64_t nblocks = (nunits + UB - 1) / UB;
   float* part = c.take<float>((size_t)B * nunits * 2 * D);
   int32_t* meta = c.take<int32_t>((size_t)B * nunits * 4);
+  float* bpart = c.take<float>((size_t)B * nblocks * D);
+  int32_t* bmeta = c.take<int32_t>((size_t)B * nblocks * 2);
   int rc = FKC_OK;
   const bool idx = perm != nullptr;
   switch (dtype) {
@@ -380,10 +576,18 @@ int launch_update(const void* x, const int32_t* perm,
       return fail(FKC_ERR_INVALID, "centroid_update: unknown dtype %d", dtype);
   }
   if (rc) return rc;
+  // With one block every run ends inside it and block partials are unused.
+  if (nblocks > 1) {
+    dim3 bgrid((unsigned)((nblocks + 3) / 4), (unsigned)B);
+    hipLaunchKernelGGL(update_blocks_kernel, bgrid, dim3(UT), 0, s, part, meta,
+                       bpart, bmeta, (int)D, (int)nunits, (int)nblocks, ctrl);
+    rc = check_launch("update_blocks");
+    if (rc) return rc;
+  }
   dim3 grid((unsigned)((nunits + 3) / 4), (unsigned)B);
   hipLaunchKernelGGL(update_merge_kernel, grid, dim3(UT), 0, s, part, meta,
-                     sums, counts, (int)K, (int)D, (int)nunits,
-                     overwrite ? 1 : 0, ctrl);
+                     bpart, bmeta, sums, counts, (int)K, (int)D, (int)nunits,
+                     (int)nblocks, overwrite ? 1 : 0, ctrl);
   return check_launch("update_merge");
 }
 

@@ -9,7 +9,8 @@
  *     except fkc_kmeans_lloyd when the caller asks for the host
  *     iteration count (see there);
  *   - allocates no device memory: scratch comes in through a caller-owned
- *     workspace whose size the matching *_workspace_bytes() reports;
+ *     workspace whose size the matching *_workspace_bytes() reports and
+ *     whose base is 256-byte aligned (hipMalloc pointers are);
  *   - returns FKC_OK (0) or a non-zero FKC_ERR_* code and never throws;
  *     fkc_last_error() then gives a message (thread-local).
  *

@@ -79,6 +79,17 @@ def test_invalid_arguments_are_rejected_without_a_device():
     rc, msg = _err(L.fkc_centroid_finalize(None, fake, fake, fake, 1, 4, 8, 1, None))
     assert rc == 1
     assert L.fkc_euclid_assign(fake, fake, None, fake, fake, 1 << 20, 10, 4, 16, 1, None) == 4
+    # a workspace that is large enough but not 256-byte aligned is refused
+    # before anything is launched
+    odd = 0x1010
+    rc, msg = _err(L.fkc_label_sort(fake, fake, fake, 1, 1000, 10, odd, 1 << 20, None))
+    assert rc == 2 and "aligned" in msg
+    rc, msg = _err(L.fkc_centroid_update_sorted(fake, fake, fake, fake, 1, 10, 4, 8, 1,
+                                                odd, 1 << 20, None))
+    assert rc == 2 and "aligned" in msg
+    rc, msg = _err(L.fkc_kmeans_lloyd(fake, fake, fake, 1, 100, 4, 8, 1, 3, 0.0, odd,
+                                      1 << 24, None, None, None))
+    assert rc == 2 and "aligned" in msg
 
 
 def test_empty_inputs_are_no_ops():

@@ -196,6 +196,27 @@ def test_verbose_path_equals_fused_loop(capsys):
     assert torch.equal(a[1], b[1])
 
 
+@pytest.mark.parametrize("B,N,K,D,dtype", [(1, 600000, 2, 16, "f16"), (2, 300000, 5, 72, "bf16")])
+def test_few_clusters_many_points(B, N, K, D, dtype):
+    """Clusters of 10^5 points: runs over many units and blocks in the fused
+    loop's overwrite-mode update; fused loop == per-op path, and the oracle
+    bar holds."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    rng = np.random.default_rng(N + K)
+    centres = 3 * rng.standard_normal((K, D)).astype(np.float32)
+    blob = rng.integers(0, K, (B, N))
+    x = O.from_f32(centres[blob] + rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    init = np.ascontiguousarray(x[:, :K])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a = batch_kmeans_Euclid(xt, K, max_iters=4, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, K, max_iters=4, init_centroids=it, verbose=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    o_ids, o_c, o_n = O.kmeans(x, K, 4, 0.0, init, dtype)
+    assert (a[0].cpu().numpy() != o_ids).mean() < 1e-3
+    gc, oc = O.to_f64(_N(a[1], dtype), dtype), O.to_f64(o_c, dtype)
+    assert np.linalg.norm(gc - oc) / np.linalg.norm(oc) < 1e-2
+
+
 def test_deterministic_loop():
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c3"]

@@ -120,6 +120,39 @@ def test_update_zipf_skew_and_empty_clusters():
     assert np.all(s[ec == 0] == 0)
 
 
+# Sorted label layouts made of long runs: a run over many 128-row units and
+# 64-unit blocks exercises the two-level run merge.  (label, length) per run.
+LONG_RUNS = [
+    ("one_run", [[(0, 600000)]], 1, 64, "f16"),
+    ("block_aligned", [[(0, 16384), (1, 70000)]], 2, 128, "bf16"),
+    ("mid_block", [[(0, 1000), (1, 300000), (2, 77), (3, 50000), (5, 123456)]], 6, 40, "f32"),
+    ("two_rows", [[(0, 200000), (2, 100)], [(1, 57), (2, 200043)]], 3, 16, "f16"),
+    ("unit_edges", [[(0, 128 * 64 * 3 - 1), (1, 1), (2, 128 * 64 + 128)]], 3, 8, "bf16"),
+]
+
+
+@pytest.mark.parametrize("name,runs,K,D,dtype", LONG_RUNS, ids=[r[0] for r in LONG_RUNS])
+def test_update_long_runs(name, runs, K, D, dtype):
+    from flash_kmeans_cuda import _C
+    B = len(runs)
+    N = sum(n for _, n in runs[0])
+    rng = np.random.default_rng(len(name))
+    s_ids = np.stack([np.concatenate([np.full(n, k, np.int32) for k, n in row]) for row in runs])
+    perm = np.stack([rng.permutation(N).astype(np.int32) for _ in range(B)])
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    es, ec = O.update_sorted_indexed(x, perm, s_ids, K, dtype)
+    outs = []
+    for _ in range(2):
+        sums = torch.full((B, K, D), 0.25, device="cuda")
+        cnt = torch.full((B, K), 2, device="cuda", dtype=torch.int32)
+        _C.centroid_update_sorted_indexed(_t(x, dtype), _t(perm), _t(s_ids), sums, cnt)
+        outs.append((_np(sums), _np(cnt)))
+    assert np.array_equal(outs[0][1], ec + 2)
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32))
+    tol = 1e-6 * np.maximum(ec[..., None], 1) * np.abs(O.to_f64(x, dtype)).max()
+    assert np.all(np.abs(outs[0][0] - 0.25 - es) <= tol + 1e-4)
+
+
 def test_update_adds_into_existing_sums_and_is_deterministic():
     from flash_kmeans_cuda import _C
     x, ids, s_ids, perm = _update_case(2, 9000, 37, 64, "bf16", seed=4)
