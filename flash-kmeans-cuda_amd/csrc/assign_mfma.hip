@@ -20,19 +20,26 @@
 //                 matrix core holding the score to maximise; centroids past K
 //                 get -inf and can never win.
 // Lane l holds column (point) l%16 and rows 4(l/16)+r, r = 0..3: four scores
-// of one point against consecutive centroids.  A lane keeps a running
-// (best, index); a tile's max is compared once, and only when it beats the
-// best does the lane look for the first matching slot.  The four lanes that
-// share a point (l, l+16, l+32, l+48) merge at the end with the lowest-index
-// rule.  Feature widths that are not a multiple of 32 are zero-padded in
-// registers and LDS (zeros add nothing to a dot product).
+// of one point against consecutive centroids.  A lane keeps its best score
+// and the 16-centroid block where it first appeared (two max3 and a
+// compare-select per four scores, branch-free, so the vector ALU stays well
+// under the matrix core's time per score and the next block's MFMA chain
+// issues under this block's fold).  At the end the four lanes that share a
+// point (l, l+16, l+32, l+48) merge with the lowest-index rule, and the
+// winner's four candidate rows are scored again by the same MFMA chain to
+// pick the first maximal one.  For K <= FKC_EXACT_MAX_K the loop tracks the
+// exact index instead (the re-score would cost more than it saves).
+// Feature widths that are not a multiple of 32 are zero-padded in registers
+// and LDS (zeros add nothing to a dot product).
 //
-// Workgroup: 4 waves x PT point tiles x 16 points (PT chosen per grid size).  Centroids pass through LDS
-// in stages of 64 rows (row stride DP+8 halves: the 16-byte pad spreads the
-// rows a ds_read_b128 touches over distinct banks), double-buffered with one
-// barrier per stage; the next stage's global loads are in flight while the
-// matrix cores work on the current one.  Centroid rows past K re-read row
-// K-1 instead of branching (their scores are masked).
+// Workgroup: 4 waves x PT point tiles x 16 points (PT chosen per grid size).
+// Centroids pass through LDS in double-buffered stages with one barrier per
+// stage; the next stage's loads are in flight while the matrix cores work
+// on the current one.  For D = 128 / 256 the stages are direct global->LDS
+// loads into unpadded, XOR-permuted rows (no staging registers, no bank
+// conflicts); other widths stage through VGPRs into rows padded by 16 bytes.
+// Centroid rows past K re-read row K-1 instead of branching (their scores
+// are masked to -inf).
 #include "device_util.hpp"
 #include "fkc_internal.hpp"
 
@@ -46,7 +53,24 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int KC = 64;        // centroid rows per LDS stage
+// Compile-time tunables (defaults measured on MI355X at the benchmark
+// shapes): FKC_AB, minimum waves per SIMD asked of the register allocator
+// for the lighter variants; FKC_EXACT_MAX_K, largest K that tracks the exact
+// index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
+// FKC_KC_DMA, centroid rows per direct stage (D <= 128).
+#ifndef FKC_AB
+#define FKC_AB 2
+#endif
+#ifndef FKC_EXACT_MAX_K
+#define FKC_EXACT_MAX_K 512
+#endif
+#ifndef FKC_USE_DMA
+#define FKC_USE_DMA 1
+#endif
+#ifndef FKC_KC_DMA
+#define FKC_KC_DMA 64
+#endif
+constexpr int KC = 64;  // centroid rows per register-staged LDS stage
 constexpr int THREADS = 256;  // 4 waves
 
 template <int DT>
@@ -65,22 +89,47 @@ __device__ inline f32x4 mfma16<FKC_BF16>(u32x4 a, u32x4 b, f32x4 c) {
       0);
 }
 
-// Fold four scores (centroids kt..kt+3) into the running (best, index).
-__device__ inline void fold4(const f32x4& acc, float& best, int& bidx,
-                             int kt) {
-  const float m = fmaxf(fmaxf(fmaxf(acc[0], acc[1]), acc[2]), acc[3]);
-  if (m > best) {  // strict: an equal score seen later has a larger index
-    const int sel =
-        acc[0] == m ? 0 : (acc[1] == m ? 1 : (acc[2] == m ? 2 : 3));
-    best = m;
-    bidx = kt + sel;
-  }
+// Slot permutation of unpadded stage rows: row r keeps feature segment v in
+// slot v ^ swz(r).  Sixteen consecutive rows (one fragment read) then cover
+// 16 distinct 16-byte bank groups for any SEGS = 4, 8, 16, 32.
+template <int SEGS>
+__device__ constexpr int swz(int r) {
+  return SEGS >= 16 ? (r & 15) : ((r & 15) / (16 / SEGS));
+}
+
+// Running maximum of a lane's scores.  The main loop keeps, per lane and
+// point tile, only the best score and the first 16-centroid block that
+// reached it (a wave-uniform value): two max3 and a compare-select per four
+// scores, with no branch, so the matrix-core chain of the next block can
+// issue under the fold of this one.  Which of the lane's four rows in that
+// block won is settled once at the end.
+__device__ inline void fold_block(const f32x4& acc, float& best, int& bblk,
+                                  int blk) {
+  const float nb = fmaxf(fmaxf(fmaxf(fmaxf(best, acc[0]), acc[1]), acc[2]),
+                         acc[3]);
+  bblk = nb > best ? blk : bblk;  // strict: equal later scores keep the first
+  best = nb;
+}
+
+// Exact running (best, index) over a lane's four scores of block rows
+// kt..kt+3, the first maximal row winning; used when K is small, where the
+// end-of-loop recompute would cost more than it saves.
+__device__ inline void fold_exact(const f32x4& acc, float& best, int& bidx,
+                                  int kt) {
+  const float nb = fmaxf(fmaxf(fmaxf(fmaxf(best, acc[0]), acc[1]), acc[2]),
+                         acc[3]);
+  const int j = acc[0] == nb ? 0 : (acc[1] == nb ? 1 : (acc[2] == nb ? 2 : 3));
+  bidx = nb > best ? kt + j : bidx;
+  best = nb;
 }
 
 // DS2: 32-feature steps (padded width DP = 32*DS2 >= D); PT: 16-point tiles
-// per wave.  D % 8 == 0 so every 8-feature segment is a 16-byte load.
-template <int DT, int DS2, int PT>
-__global__ void __launch_bounds__(THREADS, (PT * DS2 <= 16) ? 2 : 1)
+// per wave; PAD: D < DP, so segments past D read as zeros (a compile-time
+// flag: the unpadded variants carry no per-load condition); EXACT: track
+// the exact index in the loop instead of re-scoring at the end.  D % 8 == 0
+// so every 8-feature segment is a 16-byte load.
+template <int DT, int DS2, int PT, bool PAD, bool EXACT>
+__global__ void __launch_bounds__(THREADS, (PT * DS2 <= 16) ? FKC_AB : 1)
 assign_mfma_kernel(const uint16_t* __restrict__ x,
                    const uint16_t* __restrict__ cent,
                    const float* __restrict__ c_sq, int32_t* __restrict__ ids,
@@ -95,15 +144,16 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
   constexpr int PTS_WG = 4 * PTS_WAVE;
   constexpr int NT = KC / 16;
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds_c[2][KC * ROW];
-  __shared__ __attribute__((aligned(16))) float lds_q[2][KC];
+  // Direct-to-LDS stages measured faster for D = 128 and 256 only (at D = 64
+  // the short stages leave their latency exposed).
+  constexpr bool DMA = FKC_USE_DMA && !PAD && (DS2 == 4 || DS2 == 8);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, g = lane >> 4;
   const int b = blockIdx.y;
   const int dsegs = D / 8;          // real segments per row
-  const bool padded = dsegs != SEGS;
+  constexpr bool padded = PAD;
   const uint16_t* xb = x + (size_t)b * N * D;
   const uint16_t* cb = cent + (size_t)b * K * D;
   const float* qb = c_sq + (size_t)b * K;
@@ -124,101 +174,293 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
   }
 
   float best[PT];
-  int bidx[PT];
+  int bblk[PT];
 #pragma unroll
   for (int p = 0; p < PT; ++p) {
     best[p] = -INFINITY;
-    bidx[p] = 0;
+    bblk[p] = 0;
   }
 
-  u32x4 pf[PPT];
-  float pq = 0.f;
-  const int nchunks = (K + KC - 1) / KC;
+  if constexpr (DMA) {
+    // Direct global->LDS stages.  A wave's load instruction writes 64 lanes
+    // x 16 bytes to consecutive LDS, so a stage row is stored unpadded as
+    // SEGS 16-byte slots, slot v holding feature segment v ^ swz(row): the
+    // sixteen rows a fragment read touches then fall on distinct banks.  The
+    // two stage buffers are separate arrays, so the compiler can tell that
+    // loads into one do not alias reads from the other and need not wait
+    // for them.  Each lane's source offset within a stage is fixed, so a
+    // stage costs one scalar address update; only the last, partial stage
+    // clamps rows to K-1.  c_sq lands raw and each wave scales (and masks
+    // past K) its own share once its loads are in, before the barrier.
+    constexpr int KCD = DS2 <= 4 ? FKC_KC_DMA : 64;
+    constexpr int ROWB = DP * 2;
+    constexpr int STAGE = KCD * ROWB;
+    constexpr int LOADS = STAGE / (THREADS * 16);
+    constexpr int QW = KCD / 4;  // c_sq entries loaded per wave
+    static_assert(STAGE % (THREADS * 16) == 0 && QW <= 64, "stage split");
+    __shared__ __attribute__((aligned(1024))) uint8_t s_c0[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_c1[STAGE];
+    __shared__ __attribute__((aligned(256))) float s_q0[KCD];
+    __shared__ __attribute__((aligned(256))) float s_q1[KCD];
+    typedef __attribute__((address_space(1))) void gvoid;
+    typedef __attribute__((address_space(3))) void lvoid;
 
-  auto gload = [&](int chunk) {
-    const int kb = chunk * KC;
+    static_assert((ROWB & (ROWB - 1)) == 0, "power-of-two stage rows");
+    uint32_t soff[LOADS];  // row * ROWB + permuted segment byte
 #pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      const int i = tid + j * THREADS;
-      if (PIECES % THREADS == 0 || i < PIECES) {
-        const int r = i / SEGS, sg = i % SEGS;
-        const int k = min(kb + r, K - 1);
-        const u32x4* row = reinterpret_cast<const u32x4*>(cb + (size_t)k * D);
-        pf[j] = (!padded || sg < dsegs) ? row[sg] : u32x4{0u, 0u, 0u, 0u};
-      }
+    for (int j = 0; j < LOADS; ++j) {
+      const int pos = (wave * LOADS + j) * 1024 + lane * 16;
+      const int r = pos / ROWB, v = (pos % ROWB) / 16;
+      soff[j] = (uint32_t)(r * ROWB + (v ^ swz<SEGS>(r)) * 16);
     }
-    if (tid < KC) {
-      const int k = kb + tid;
-      pq = (k < K) ? -0.5f * qb[k] : -INFINITY;
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      const int i = tid + j * THREADS;
-      if (PIECES % THREADS == 0 || i < PIECES) {
-        const int r = i / SEGS, sg = i % SEGS;
-        *reinterpret_cast<u32x4*>(&lds_c[buf][r * ROW + sg * 8]) = pf[j];
-      }
-    }
-    if (tid < KC) lds_q[buf][tid] = pq;
-  };
+    const int qi = wave * QW + lane;  // this lane's c_sq slot (lane < QW)
+    const int sw = swz<SEGS>(col);    // rows 16t + col share it
+    const int nch = (K + KCD - 1) / KCD;
+    const char* cbase = reinterpret_cast<const char*>(cb);
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
-  for (int chunk = 0; chunk < nchunks; ++chunk) {
-    const int buf = chunk & 1;
-    if (chunk + 1 < nchunks) gload(chunk + 1);
-    const uint16_t* lc = lds_c[buf];
-    const float* lq = lds_q[buf];
+    auto issue = [&](int chunk, uint8_t* dc, float* dq) {
+      const int kb = chunk * KCD;
+      const char* src = cbase + (size_t)kb * ROWB;
+      const bool tail = kb + KCD > K;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const f32x4 cinit = *reinterpret_cast<const f32x4*>(lq + 16 * t + 4 * g);
-      const u32x4* arow =
-          reinterpret_cast<const u32x4*>(lc + (16 * t + col) * ROW) + g;
-      u32x4 a[DS2];
-#pragma unroll
-      for (int s = 0; s < DS2; ++s) a[s] = arow[4 * s];
-      f32x4 acc[PT];
-#pragma unroll
-      for (int s = 0; s < DS2; ++s) {
-#pragma unroll
-        for (int p = 0; p < PT; ++p)
-          acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? cinit : acc[p]);
+      for (int j = 0; j < LOADS; ++j) {
+        uint32_t off = soff[j];
+        if (tail) {
+          const int r = (int)(off / ROWB);
+          off = (uint32_t)(min(r, K - 1 - kb) * ROWB) + off % ROWB;
+        }
+        __builtin_amdgcn_global_load_lds(
+            (gvoid*)(src + off), (lvoid*)(dc + (wave * LOADS + j) * 1024), 16,
+            0, 0);
       }
-      const int kt = chunk * KC + 16 * t + 4 * g;
+      if (lane < QW) {
+        const uint32_t k = (uint32_t)min(qi, K - 1 - kb);
+        __builtin_amdgcn_global_load_lds((gvoid*)(qb + kb + k),
+                                         (lvoid*)(dq + wave * QW), 4, 0, 0);
+      }
+    };
+    // After this wave's loads have landed: scale its c_sq share in place.
+    auto fixq = [&](int chunk, float* dq) {
+      if (lane < QW) {
+        const int k = chunk * KCD + qi;
+        dq[qi] = k < K ? -0.5f * dq[qi] : -INFINITY;
+      }
+    };
+    auto compute = [&](int chunk, const uint8_t* lc, const float* lq) {
+      const int kb = chunk * KCD;
 #pragma unroll
-      for (int p = 0; p < PT; ++p) fold4(acc[p], best[p], bidx[p], kt);
-    }
-    if (chunk + 1 < nchunks) lstore(buf ^ 1);
+      for (int t = 0; t < KCD / 16; ++t) {
+        const f32x4 cinit =
+            *reinterpret_cast<const f32x4*>(lq + 16 * t + 4 * g);
+        const uint8_t* arow = lc + (16 * t + col) * ROWB;
+        u32x4 a[DS2];
+#pragma unroll
+        for (int s = 0; s < DS2; ++s)
+          a[s] = *reinterpret_cast<const u32x4*>(arow + (((4 * s + g) ^ sw) * 16));
+        f32x4 acc[PT];
+#pragma unroll
+        for (int s = 0; s < DS2; ++s) {
+#pragma unroll
+          for (int p = 0; p < PT; ++p)
+            acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? cinit : acc[p]);
+        }
+        const int blk = kb + 16 * t;
+#pragma unroll
+        for (int p = 0; p < PT; ++p) {
+          if constexpr (EXACT)
+            fold_exact(acc[p], best[p], bblk[p], blk + 4 * g);
+          else
+            fold_block(acc[p], best[p], bblk[p], blk);
+        }
+      }
+    };
+
+    issue(0, s_c0, s_q0);
+    __builtin_amdgcn_s_waitcnt(0);
+    fixq(0, s_q0);
     __syncthreads();
+    for (int chunk = 0; chunk < nch; chunk += 2) {
+      if (chunk + 1 < nch) issue(chunk + 1, s_c1, s_q1);
+      compute(chunk, s_c0, s_q0);
+      __builtin_amdgcn_s_waitcnt(0);
+      if (chunk + 1 < nch) fixq(chunk + 1, s_q1);
+      __syncthreads();
+      if (chunk + 1 >= nch) break;
+      if (chunk + 2 < nch) issue(chunk + 2, s_c0, s_q0);
+      compute(chunk + 1, s_c1, s_q1);
+      __builtin_amdgcn_s_waitcnt(0);
+      if (chunk + 2 < nch) fixq(chunk + 2, s_q0);
+      __syncthreads();
+    }
+  } else {
+    // Stages through VGPRs into padded LDS rows (row stride DP + 8 halves).
+    __shared__ __attribute__((aligned(16))) uint16_t lds_c[2][KC * ROW];
+    __shared__ __attribute__((aligned(16))) float lds_q[2][KC];
+    u32x4 pf[PPT];
+    float pq = 0.f;  // raw c_sq of the prefetched stage (scaled when stored)
+    const int nchunks = (K + KC - 1) / KC;
+
+    auto gload = [&](int chunk) {
+      const int kb = chunk * KC;
+  #pragma unroll
+      for (int j = 0; j < PPT; ++j) {
+        const int i = tid + j * THREADS;
+        if (PIECES % THREADS == 0 || i < PIECES) {
+          const int r = i / SEGS, sg = i % SEGS;
+          const int k = min(kb + r, K - 1);
+          const u32x4* row = reinterpret_cast<const u32x4*>(cb + (size_t)k * D);
+          pf[j] = (!padded || sg < dsegs) ? row[sg] : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      // Only the load is issued here; using the value (scale, mask) waits for
+      // it, which would stall this wave before the stage's matrix work.
+      if (tid < KC) pq = qb[min(kb + tid, K - 1)];
+    };
+    auto lstore = [&](int buf, int chunk) {
+      const int kb = chunk * KC;
+  #pragma unroll
+      for (int j = 0; j < PPT; ++j) {
+        const int i = tid + j * THREADS;
+        if (PIECES % THREADS == 0 || i < PIECES) {
+          const int r = i / SEGS, sg = i % SEGS;
+          *reinterpret_cast<u32x4*>(&lds_c[buf][r * ROW + sg * 8]) = pf[j];
+        }
+      }
+      if (tid < KC) {
+        const int k = kb + tid;
+        lds_q[buf][tid] = k < K ? -0.5f * pq : -INFINITY;
+      }
+    };
+
+    gload(0);
+    lstore(0, 0);
+    __syncthreads();
+
+    for (int chunk = 0; chunk < nchunks; ++chunk) {
+      const int buf = chunk & 1;
+      if (chunk + 1 < nchunks) gload(chunk + 1);
+      const uint16_t* lc = lds_c[buf];
+      const float* lq = lds_q[buf];
+  #pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4 cinit = *reinterpret_cast<const f32x4*>(lq + 16 * t + 4 * g);
+        const u32x4* arow =
+            reinterpret_cast<const u32x4*>(lc + (16 * t + col) * ROW) + g;
+        u32x4 a[DS2];
+#pragma unroll
+        for (int s = 0; s < DS2; ++s) a[s] = arow[4 * s];
+        f32x4 acc[PT];
+#pragma unroll
+        for (int s = 0; s < DS2; ++s) {
+#pragma unroll
+          for (int p = 0; p < PT; ++p)
+            acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? cinit : acc[p]);
+        }
+        const int blk = chunk * KC + 16 * t;
+#pragma unroll
+        for (int p = 0; p < PT; ++p) {
+          if constexpr (EXACT)
+            fold_exact(acc[p], best[p], bblk[p], blk + 4 * g);
+          else
+            fold_block(acc[p], best[p], bblk[p], blk);
+        }
+      }
+      if (chunk + 1 < nchunks) lstore(buf ^ 1, chunk + 1);
+      __syncthreads();
+    }
   }
 
+  // Settle each point: the four lanes sharing it (g = 0..3) hold the best
+  // score of their rows and the block where it first appeared; the winner
+  // is the higher score, ties to the lower candidate base blk + 4g (the four
+  // candidate ranges do not interleave).  Then the four candidates
+  // base + r are scored again with the same instruction, operands and
+  // accumulator seed as in the loop, one MFMA chain per r with row i holding
+  // point i's candidate, and the first r reaching the maximum of the
+  // diagonal wins.
+  if constexpr (EXACT) {
+#pragma unroll
+    for (int p = 0; p < PT; ++p) {
+      float bv = best[p];
+      int bi = bblk[p];
+#pragma unroll
+      for (int off = 16; off <= 32; off <<= 1) {
+        const float ob = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ob > bv || (ob == bv && oi < bi)) {
+          bv = ob;
+          bi = oi;
+        }
+      }
+      const int n = n0 + 16 * p + col;
+      if (g == 0 && n < N) ids[(size_t)b * N + n] = bi;
+    }
+    return;
+  }
 #pragma unroll
   for (int p = 0; p < PT; ++p) {
+    float bv = best[p];
+    int base = bblk[p] + 4 * g;
 #pragma unroll
     for (int off = 16; off <= 32; off <<= 1) {
-      const float ob = __shfl_xor(best[p], off, 64);
-      const int oi = __shfl_xor(bidx[p], off, 64);
-      if (ob > best[p] || (ob == best[p] && oi < bidx[p])) {
-        best[p] = ob;
-        bidx[p] = oi;
+      const float ob = __shfl_xor(bv, off, 64);
+      const int obase = __shfl_xor(base, off, 64);
+      if (ob > bv || (ob == bv && obase < base)) {
+        bv = ob;
+        base = obase;
+      }
+    }
+    // Accumulator rows 4g+j of this lane belong to point 4g+j of the tile.
+    int rbase[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rbase[j] = __shfl(base, 4 * g + j, 64);
+    const int e = col & 3;  // this lane's diagonal element when g == col/4
+    float dv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      f32x4 acc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = rbase[j] + r;
+        acc[j] = k < K ? -0.5f * qb[k] : -INFINITY;
+      }
+      const int kr = min(base + r, K - 1);
+      const u32x4* crow = reinterpret_cast<const u32x4*>(cb + (size_t)kr * D);
+#pragma unroll
+      for (int s = 0; s < DS2; ++s) {
+        const int seg = 4 * s + g;
+        const u32x4 a =
+            (!padded || seg < dsegs) ? crow[seg] : u32x4{0u, 0u, 0u, 0u};
+        acc = mfma16<DT>(a, xr[p][s], acc);
+      }
+      float d = acc[0];
+      d = e == 1 ? acc[1] : d;
+      d = e == 2 ? acc[2] : d;
+      d = e == 3 ? acc[3] : d;
+      dv[r] = d;
+    }
+    int rr = 0;
+    float m = dv[0];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) {
+      if (dv[r] > m) {
+        m = dv[r];
+        rr = r;
       }
     }
     const int n = n0 + 16 * p + col;
-    if (g == 0 && n < N) ids[(size_t)b * N + n] = bidx[p];
+    if (g == (col >> 2) && n < N) ids[(size_t)b * N + n] = base + rr;
   }
 }
 
-template <int DT, int DS2, int PT>
+template <int DT, int DS2, int PT, bool PAD, bool EXACT>
 int launch_mfma_t(const void* x, const void* c, const float* c_sq,
                   int32_t* ids, int64_t B, int64_t N, int64_t K, int64_t D,
                   const int32_t* ctrl, hipStream_t s) {
   constexpr int PTS_WG = 4 * PT * 16;
   dim3 grid((unsigned)((N + PTS_WG - 1) / PTS_WG), (unsigned)B);
-  hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT>), grid, dim3(THREADS),
+  hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
+                     dim3(THREADS),
                      0, s, static_cast<const uint16_t*>(x),
                      static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
                      (int)K, (int)D, ctrl);
@@ -230,45 +472,49 @@ using MfmaLauncher = int (*)(const void*, const void*, const float*, int32_t*,
                              const int32_t*, hipStream_t);
 
 template <int DT, int DS2, int PT>
-constexpr MfmaLauncher entry() {
-  if constexpr (PT * DS2 * 4 <= 64 || (PT == 8 && (DS2 == 2 || DS2 == 4)))
-    return &launch_mfma_t<DT, DS2, PT>;
-  else
+constexpr MfmaLauncher entry(bool pad, bool exact) {
+  if constexpr (PT * DS2 * 4 <= 64) {
+    if (exact)
+      return pad ? &launch_mfma_t<DT, DS2, PT, true, true>
+                 : &launch_mfma_t<DT, DS2, PT, false, true>;
+    return pad ? &launch_mfma_t<DT, DS2, PT, true, false>
+               : &launch_mfma_t<DT, DS2, PT, false, false>;
+  } else {
     return nullptr;
+  }
 }
 
-// pt: 16-point tiles per wave (1, 2, 4, or 8 for D = 64 / 128 only).
-// Variants keep the point registers (PT * DS2 * 4 VGPRs) at <= 64.
+// pt: 16-point tiles per wave (1, 2 or 4).  Variants keep the point
+// registers (PT * DS2 * 4 VGPRs) at <= 64.
 template <int DT, int DS2>
-MfmaLauncher by_pt(int pt) {
+MfmaLauncher by_pt(int pt, bool pad, bool exact) {
   switch (pt) {
-    case 1: return entry<DT, DS2, 1>();
-    case 2: return entry<DT, DS2, 2>();
-    case 4: return entry<DT, DS2, 4>();
-    case 8: return entry<DT, DS2, 8>();
+    case 1: return entry<DT, DS2, 1>(pad, exact);
+    case 2: return entry<DT, DS2, 2>(pad, exact);
+    case 4: return entry<DT, DS2, 4>(pad, exact);
     default: return nullptr;
   }
 }
 
 template <int DT>
-MfmaLauncher mfma_launcher(int ds2, int pt) {
+MfmaLauncher mfma_launcher(int ds2, int pt, bool pad, bool exact) {
   switch (ds2) {
-    case 1: return by_pt<DT, 1>(pt);
-    case 2: return by_pt<DT, 2>(pt);
-    case 3: return by_pt<DT, 3>(pt);
-    case 4: return by_pt<DT, 4>(pt);
-    case 5: return by_pt<DT, 5>(pt);
-    case 6: return by_pt<DT, 6>(pt);
-    case 7: return by_pt<DT, 7>(pt);
-    case 8: return by_pt<DT, 8>(pt);
-    case 9: return by_pt<DT, 9>(pt);
-    case 10: return by_pt<DT, 10>(pt);
-    case 11: return by_pt<DT, 11>(pt);
-    case 12: return by_pt<DT, 12>(pt);
-    case 13: return by_pt<DT, 13>(pt);
-    case 14: return by_pt<DT, 14>(pt);
-    case 15: return by_pt<DT, 15>(pt);
-    case 16: return by_pt<DT, 16>(pt);
+    case 1: return by_pt<DT, 1>(pt, pad, exact);
+    case 2: return by_pt<DT, 2>(pt, pad, exact);
+    case 3: return by_pt<DT, 3>(pt, pad, exact);
+    case 4: return by_pt<DT, 4>(pt, pad, exact);
+    case 5: return by_pt<DT, 5>(pt, pad, exact);
+    case 6: return by_pt<DT, 6>(pt, pad, exact);
+    case 7: return by_pt<DT, 7>(pt, pad, exact);
+    case 8: return by_pt<DT, 8>(pt, pad, exact);
+    case 9: return by_pt<DT, 9>(pt, pad, exact);
+    case 10: return by_pt<DT, 10>(pt, pad, exact);
+    case 11: return by_pt<DT, 11>(pt, pad, exact);
+    case 12: return by_pt<DT, 12>(pt, pad, exact);
+    case 13: return by_pt<DT, 13>(pt, pad, exact);
+    case 14: return by_pt<DT, 14>(pt, pad, exact);
+    case 15: return by_pt<DT, 15>(pt, pad, exact);
+    case 16: return by_pt<DT, 16>(pt, pad, exact);
     default: return nullptr;
   }
 }
@@ -287,8 +533,7 @@ bool assign_uses_mfma(int dtype, int64_t D) {
 // shapes).  FKC_NTILES overrides.
 static int choose_pt(int ds2, int64_t B, int64_t N) {
   const int o = ntiles_override();
-  if (o != 0 && (o * ds2 * 4 <= 64 || (o == 8 && (ds2 == 2 || ds2 == 4))))
-    return o;
+  if (o != 0 && o * ds2 * 4 <= 64) return o;
   for (int pt = 4; pt > 1; pt >>= 1) {
     if (pt * ds2 * 4 > 64) continue;
     const int64_t wgs = B * ((N + 64 * pt - 1) / (64 * pt));
@@ -303,8 +548,13 @@ int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                        hipStream_t s) {
   const int ds2 = (int)((D + 31) / 32);
   const int pt = choose_pt(ds2, B, N);
-  MfmaLauncher fn = dtype == FKC_F16 ? mfma_launcher<FKC_F16>(ds2, pt)
-                                     : mfma_launcher<FKC_BF16>(ds2, pt);
+  const bool pad = D != 32 * ds2;
+  // Re-scoring the winning block costs about one 16-centroid block per point
+  // tile; below this K the exact in-loop index is cheaper.
+  const bool exact = K <= FKC_EXACT_MAX_K;
+  MfmaLauncher fn =
+      dtype == FKC_F16 ? mfma_launcher<FKC_F16>(ds2, pt, pad, exact)
+                       : mfma_launcher<FKC_BF16>(ds2, pt, pad, exact);
   if (!fn)
     return fail(FKC_ERR_UNSUPPORTED, "assign: no MFMA variant for D=%lld",
                 (long long)D);

@@ -92,7 +92,7 @@ int launch_converge_check(const float* shift, int it, float tol, int32_t* ctrl,
 
 // FKC_ASSIGN_FORCE_SAFE=1|true: route every dtype to the fp32 VALU kernel.
 bool force_safe_assign();
-// FKC_NTILES=1|2|4|8: 16-point tiles per wave in the MFMA kernel; 0 = auto.
+// FKC_NTILES=1|2|4: 16-point tiles per wave in the MFMA kernel; 0 = auto.
 int ntiles_override();
 
 }  // namespace fkc
