@@ -57,7 +57,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // shapes): FKC_AB, minimum waves per SIMD asked of the register allocator
 // for the lighter variants; FKC_EXACT_MAX_K, largest K that tracks the exact
 // index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
-// FKC_KC_DMA, centroid rows per direct stage (D <= 128).
+// FKC_KC_DMA, centroid rows per direct stage (D <= 128); FKC_SCHED_GROUPS,
+// MFMA/VALU interleaving hints in the direct-stage loop.
 #ifndef FKC_AB
 #define FKC_AB 2
 #endif
@@ -70,6 +71,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #ifndef FKC_KC_DMA
 #define FKC_KC_DMA 64
 #endif
+#ifndef FKC_SCHED_GROUPS
+#define FKC_SCHED_GROUPS 1
+#endif
+
 constexpr int KC = 64;  // centroid rows per register-staged LDS stage
 constexpr int THREADS = 256;  // 4 waves
 
@@ -181,6 +186,17 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     bblk[p] = 0;
   }
 
+  // Fold one 16-centroid block's accumulators into the running maxima.
+  auto fold = [&](const f32x4* acc, int blk) {
+#pragma unroll
+    for (int p = 0; p < PT; ++p) {
+      if constexpr (EXACT)
+        fold_exact(acc[p], best[p], bblk[p], blk + 4 * g);
+      else
+        fold_block(acc[p], best[p], bblk[p], blk);
+    }
+  };
+
   if constexpr (DMA) {
     // Direct global->LDS stages.  A wave's load instruction writes 64 lanes
     // x 16 bytes to consecutive LDS, so a stage row is stored unpadded as
@@ -206,13 +222,13 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     typedef __attribute__((address_space(3))) void lvoid;
 
     static_assert((ROWB & (ROWB - 1)) == 0, "power-of-two stage rows");
-    uint32_t soff[LOADS];  // row * ROWB + permuted segment byte
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
+    // Source byte of load j within a stage: row * ROWB + permuted segment.
+    // Recomputed per stage (a few VALU ops) rather than held in registers.
+    auto soff = [&](int j) {
       const int pos = (wave * LOADS + j) * 1024 + lane * 16;
       const int r = pos / ROWB, v = (pos % ROWB) / 16;
-      soff[j] = (uint32_t)(r * ROWB + (v ^ swz<SEGS>(r)) * 16);
-    }
+      return (uint32_t)(r * ROWB + (v ^ swz<SEGS>(r)) * 16);
+    };
     const int qi = wave * QW + lane;  // this lane's c_sq slot (lane < QW)
     const int sw = swz<SEGS>(col);    // rows 16t + col share it
     const int nch = (K + KCD - 1) / KCD;
@@ -224,7 +240,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       const bool tail = kb + KCD > K;
 #pragma unroll
       for (int j = 0; j < LOADS; ++j) {
-        uint32_t off = soff[j];
+        uint32_t off = soff(j);
         if (tail) {
           const int r = (int)(off / ROWB);
           off = (uint32_t)(min(r, K - 1 - kb) * ROWB) + off % ROWB;
@@ -240,38 +256,78 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       }
     };
     // After this wave's loads have landed: scale its c_sq share in place.
+    // Branch-free (the 64 / QW lanes that share an entry write the same
+    // value), so no block boundary splits the stage's code: a boundary here
+    // lets the compiler sink the stage's folds below it, away from the
+    // matrix-core work they should overlap.
+    const int qf = wave * QW + (lane % QW);
     auto fixq = [&](int chunk, float* dq) {
-      if (lane < QW) {
-        const int k = chunk * KCD + qi;
-        dq[qi] = k < K ? -0.5f * dq[qi] : -INFINITY;
-      }
+      const int k = chunk * KCD + qf;
+      const float v = dq[qf];
+      dq[qf] = k < K ? -0.5f * v : -INFINITY;
     };
+    auto frag = [&](const uint8_t* lc, const float* lq, int t, u32x4* a,
+                    f32x4& ci) {
+      ci = *reinterpret_cast<const f32x4*>(lq + 16 * t + 4 * g);
+      const uint8_t* arow = lc + (16 * t + col) * ROWB;
+#pragma unroll
+      for (int s = 0; s < DS2; ++s)
+        a[s] = *reinterpret_cast<const u32x4*>(arow + (((4 * s + g) ^ sw) * 16));
+    };
+    // Software-pipelined over the stage's 16-centroid blocks: block t-1 is
+    // folded on the vector ALU while block t is on the matrix core.  For
+    // four point tiles the scheduling groups ask the compiler to interleave
+    // them (MFMA, VALU) rather than issue the whole stage's MFMAs first and
+    // its folds last, which keeps every accumulator alive at once and
+    // serialises the two units within a wave (measured: 0.86 -> 0.81 ms at
+    // N=524288, K=8192, D=128; with fewer tiles the groups cost time).
     auto compute = [&](int chunk, const uint8_t* lc, const float* lq) {
       const int kb = chunk * KCD;
+      constexpr int NTD = KCD / 16;
+      if constexpr (EXACT) {
+        // Small K: few stages, so no pipelining; blocks wholly past K (a
+        // partial last stage) are skipped.
 #pragma unroll
-      for (int t = 0; t < KCD / 16; ++t) {
-        const f32x4 cinit =
-            *reinterpret_cast<const f32x4*>(lq + 16 * t + 4 * g);
-        const uint8_t* arow = lc + (16 * t + col) * ROWB;
-        u32x4 a[DS2];
+        for (int t = 0; t < NTD; ++t) {
+          if (kb + 16 * t >= K) break;
+          u32x4 a[DS2];
+          f32x4 ci;
+          frag(lc, lq, t, a, ci);
+          f32x4 acc[PT];
 #pragma unroll
-        for (int s = 0; s < DS2; ++s)
-          a[s] = *reinterpret_cast<const u32x4*>(arow + (((4 * s + g) ^ sw) * 16));
-        f32x4 acc[PT];
+          for (int s = 0; s < DS2; ++s) {
 #pragma unroll
-        for (int s = 0; s < DS2; ++s) {
-#pragma unroll
-          for (int p = 0; p < PT; ++p)
-            acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? cinit : acc[p]);
+            for (int p = 0; p < PT; ++p)
+              acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? ci : acc[p]);
+          }
+          fold(acc, kb + 16 * t);
         }
-        const int blk = kb + 16 * t;
+      } else {
+        f32x4 prev[PT];
 #pragma unroll
-        for (int p = 0; p < PT; ++p) {
-          if constexpr (EXACT)
-            fold_exact(acc[p], best[p], bblk[p], blk + 4 * g);
-          else
-            fold_block(acc[p], best[p], bblk[p], blk);
+        for (int t = 0; t < NTD; ++t) {
+          u32x4 a[DS2];
+          f32x4 ci;
+          frag(lc, lq, t, a, ci);
+          f32x4 acc[PT];
+#pragma unroll
+          for (int s = 0; s < DS2; ++s) {
+#pragma unroll
+            for (int p = 0; p < PT; ++p)
+              acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? ci : acc[p]);
+          }
+          if (t > 0) fold(prev, kb + 16 * (t - 1));
+          if constexpr (FKC_SCHED_GROUPS && PT >= 4) {
+#pragma unroll
+            for (int i = 0; i < DS2 * PT; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+            }
+          }
+#pragma unroll
+          for (int p = 0; p < PT; ++p) prev[p] = acc[p];
         }
+        fold(prev, kb + 16 * (NTD - 1));
       }
     };
 
@@ -283,13 +339,13 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       if (chunk + 1 < nch) issue(chunk + 1, s_c1, s_q1);
       compute(chunk, s_c0, s_q0);
       __builtin_amdgcn_s_waitcnt(0);
-      if (chunk + 1 < nch) fixq(chunk + 1, s_q1);
+      fixq(chunk + 1, s_q1);  // harmless on a stage that was not loaded
       __syncthreads();
       if (chunk + 1 >= nch) break;
       if (chunk + 2 < nch) issue(chunk + 2, s_c0, s_q0);
       compute(chunk + 1, s_c1, s_q1);
       __builtin_amdgcn_s_waitcnt(0);
-      if (chunk + 2 < nch) fixq(chunk + 2, s_q0);
+      fixq(chunk + 2, s_q0);
       __syncthreads();
     }
   } else {
@@ -313,8 +369,9 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
         }
       }
       // Only the load is issued here; using the value (scale, mask) waits for
-      // it, which would stall this wave before the stage's matrix work.
-      if (tid < KC) pq = qb[min(kb + tid, K - 1)];
+      // it, which would stall this wave before the stage's matrix work.  All
+      // threads load (four per entry), so no branch splits the stage's code.
+      pq = qb[min(kb + (tid & (KC - 1)), K - 1)];
     };
     auto lstore = [&](int buf, int chunk) {
       const int kb = chunk * KC;
@@ -326,10 +383,8 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
           *reinterpret_cast<u32x4*>(&lds_c[buf][r * ROW + sg * 8]) = pf[j];
         }
       }
-      if (tid < KC) {
-        const int k = kb + tid;
-        lds_q[buf][tid] = k < K ? -0.5f * pq : -INFINITY;
-      }
+      const int k = kb + (tid & (KC - 1));
+      lds_q[buf][tid & (KC - 1)] = k < K ? -0.5f * pq : -INFINITY;
     };
 
     gload(0);
@@ -341,31 +396,31 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       if (chunk + 1 < nchunks) gload(chunk + 1);
       const uint16_t* lc = lds_c[buf];
       const float* lq = lds_q[buf];
-  #pragma unroll
-      for (int t = 0; t < NT; ++t) {
+      auto tile = [&](int t, f32x4* acc) {
         const f32x4 cinit = *reinterpret_cast<const f32x4*>(lq + 16 * t + 4 * g);
         const u32x4* arow =
             reinterpret_cast<const u32x4*>(lc + (16 * t + col) * ROW) + g;
         u32x4 a[DS2];
 #pragma unroll
         for (int s = 0; s < DS2; ++s) a[s] = arow[4 * s];
-        f32x4 acc[PT];
 #pragma unroll
         for (int s = 0; s < DS2; ++s) {
 #pragma unroll
           for (int p = 0; p < PT; ++p)
             acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? cinit : acc[p]);
         }
-        const int blk = chunk * KC + 16 * t;
+      };
+      // (Folding block t-1 under block t, as the direct-stage path does,
+      // measured no faster here.)
 #pragma unroll
-        for (int p = 0; p < PT; ++p) {
-          if constexpr (EXACT)
-            fold_exact(acc[p], best[p], bblk[p], blk + 4 * g);
-          else
-            fold_block(acc[p], best[p], bblk[p], blk);
-        }
+      for (int t = 0; t < NT; ++t) {
+        f32x4 acc[PT];
+        tile(t, acc);
+        fold(acc, chunk * KC + 16 * t);
       }
-      if (chunk + 1 < nchunks) lstore(buf ^ 1, chunk + 1);
+      // Unconditional (after the last stage it fills the idle buffer with
+      // data nobody reads), so no branch splits the stage's code.
+      lstore(buf ^ 1, chunk + 1);
       __syncthreads();
     }
   }
