@@ -22,6 +22,11 @@ Reported:
                         the reference)
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c5]
+       python bench.py --report        per-config table (c1..c5): assign TFLOPS,
+                                       ms/iter (steady state and one-iteration
+                                       call), roofline fraction ideal/measured
+       python bench.py --traffic-probe / --lloyd-probe   workloads for
+                                       rocprofv3 --pmc runs (see profiles/)
 """
 
 from __future__ import annotations
@@ -107,6 +112,114 @@ def _traffic_probe(cfg) -> int:
     return 0
 
 
+def _lloyd_probe(cfg) -> int:
+    """Kernels for per-kernel rocprofv3 --pmc runs over a whole Lloyd
+    iteration: the calibration copy of _traffic_probe, then one warm-up and
+    three single-iteration batch_kmeans_Euclid calls on the configuration."""
+    import torch
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    src = torch.ones(COPY_FLOATS, device="cuda")
+    dst = torch.empty_like(src)
+    torch.add(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    x_np, init_np = synth.make(cfg)
+    x = synth.to_torch(x_np, cfg.dtype)
+    init = synth.to_torch(init_np, cfg.dtype)
+    for _ in range(4):
+        batch_kmeans_Euclid(x, cfg.K, max_iters=1, tol=0.0, init_centroids=init)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": COPY_FLOATS * 4, "copy_bytes_written": COPY_FLOATS * 4,
+                      "lloyd_calls": 4, "config": cfg.name}))
+    return 0
+
+
+def _ideal_ms(cfg) -> tuple[float, float, float]:
+    """(assign flops, bytes moved per iteration, ideal ms per iteration) from
+    the algorithmic work: 2BNKD flops at the MFMA peak (VALU fp32 peak for
+    fp32) plus the iteration's bytes at the HBM peak.  Bytes: assign
+    s*BND + s*BKD + 4BK + 4BN; sort, update, finalize, c_sq
+    s*BND + 20BN + (3s+8)*BKD + 16BK."""
+    B, N, K, D = cfg.B, cfg.N, cfg.K, cfg.D
+    s = 4 if cfg.dtype == "f32" else 2
+    flops = 2.0 * B * N * K * D
+    byts = (s * B * N * D + s * B * K * D + 4 * B * K + 4 * B * N
+            + s * B * N * D + 20 * B * N + (3 * s + 8) * B * K * D + 16 * B * K)
+    peak = 157.3e12 if cfg.dtype == "f32" else PEAK_TFLOPS_F16 * 1e12
+    return flops, byts, (flops / peak + byts / (PEAK_HBM_GBS * 1e9)) * 1e3
+
+
+def _report(configs) -> int:
+    """Per-configuration measurements (one JSON line each, then a markdown
+    table): assign alone (median of 7 x 10 launches, HIP events), the Lloyd
+    loop's steady state (cfg.iters iterations, tol = 0, per iteration), the
+    reference's methodology (one whole call with max_iters=1, best of 5), and
+    the roofline fraction ideal / measured per iteration."""
+    import statistics
+    import torch
+    from flash_kmeans_cuda import _C, batch_kmeans_Euclid, synth
+    from flash_kmeans_cuda.ops import row_sqnorm
+    rows = []
+    for name in configs:
+        cfg = synth.CONFIGS[name]
+        x_np, init_np = synth.make(cfg)
+        x = synth.to_torch(x_np, cfg.dtype)
+        init = synth.to_torch(init_np, cfg.dtype)
+        csq = row_sqnorm(init)
+        ids = torch.empty((cfg.B, cfg.N), dtype=torch.int32, device="cuda")
+        empty = torch.empty(0, device="cuda")
+        xsq = row_sqnorm(x) if cfg.dtype == "f32" else empty
+        for _ in range(3):
+            _C.euclid_assign(x, init, xsq, csq, ids)
+        times = []
+        for _ in range(7):
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                _C.euclid_assign(x, init, xsq, csq, ids)
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / 10)
+        assign_ms = statistics.median(times)
+        batch_kmeans_Euclid(x, cfg.K, max_iters=2, tol=0.0, init_centroids=init)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        batch_kmeans_Euclid(x, cfg.K, max_iters=cfg.iters, tol=0.0, init_centroids=init)
+        torch.cuda.synchronize()
+        steady = (time.perf_counter() - t0) * 1e3 / cfg.iters
+        one = []
+        for _ in range(5):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            batch_kmeans_Euclid(x, cfg.K, max_iters=1, tol=0.0, init_centroids=init)
+            torch.cuda.synchronize()
+            one.append((time.perf_counter() - t0) * 1e3)
+        flops, byts, ideal = _ideal_ms(cfg)
+        row = {
+            "config": name, "B": cfg.B, "N": cfg.N, "K": cfg.K, "D": cfg.D,
+            "dtype": cfg.dtype, "assign_ms": round(assign_ms, 5),
+            "assign_tflops": round(flops / assign_ms / 1e9, 1),
+            "ms_per_iter_steady": round(steady, 5),
+            "ms_per_iter_ref_method": round(min(one), 5),
+            "ideal_ms_per_iter": round(ideal, 5),
+            "roofline_frac": round(ideal / steady, 4),
+            "ref_ms_per_iter": REF_MS_PER_ITER.get(name),
+            "ref_assign_tflops": REF_ASSIGN_TFLOPS.get(name),
+        }
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+    print("| config | (B, N, K, D) dtype | assign ms | assign TFLOP/s | ms/iter steady | "
+          "ms/iter one call | ideal ms/iter | ideal/measured | reference ms/iter (RTX 4090) |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
+    for r in rows:
+        print(f"| {r['config']} | ({r['B']}, {r['N']}, {r['K']}, {r['D']}) {r['dtype']} | "
+              f"{r['assign_ms']:.4f} | {r['assign_tflops']:.1f} | {r['ms_per_iter_steady']:.4f} | "
+              f"{r['ms_per_iter_ref_method']:.4f} | {r['ideal_ms_per_iter']:.4f} | "
+              f"{r['roofline_frac']:.3f} | {r['ref_ms_per_iter'] or '—'} |", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,6 +231,11 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one elementwise copy kernel of "
                          "known size (calibration), then 3 assign launches")
+    ap.add_argument("--lloyd-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: the calibration copy, then 4 "
+                         "one-iteration Lloyd calls")
+    ap.add_argument("--report", nargs="?", const="c1,c2,c3,c4,c5", default=None,
+                    help="per-configuration table (comma-separated config names)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -130,9 +248,13 @@ def main() -> int:
     import torch
     from flash_kmeans_cuda import _lib, batch_kmeans_Euclid, synth
 
+    if args.report:
+        return _report(args.report.split(","))
     cfg = synth.CONFIGS[args.config]
     if args.traffic_probe:
         return _traffic_probe(cfg)
+    if args.lloyd_probe:
+        return _lloyd_probe(cfg)
     x_np, init_np = synth.make(cfg)
     x = synth.to_torch(x_np, cfg.dtype)
     init = synth.to_torch(init_np, cfg.dtype)
