@@ -48,6 +48,7 @@ KERNEL_SOURCES = [
     "label_sort.hip",
     "update.hip",
     "finalize.hip",
+    "quality.hip",
 ]
 HOST_SOURCES = ["capi.cpp"]
 

@@ -134,7 +134,7 @@ __device__ inline void fold_exact(const f32x4& acc, float& best, int& bidx,
 // the exact index in the loop instead of re-scoring at the end.  D % 8 == 0
 // so every 8-feature segment is a 16-byte load.
 template <int DT, int DS2, int PT, bool PAD, bool EXACT>
-__global__ void __launch_bounds__(THREADS, (PT * DS2 <= 16) ? FKC_AB : 1)
+__global__ void __launch_bounds__(THREADS, (PT * DS2 <= 16 && DS2 <= 9) ? FKC_AB : 1)
 assign_mfma_kernel(const uint16_t* __restrict__ x,
                    const uint16_t* __restrict__ cent,
                    const float* __restrict__ c_sq, int32_t* __restrict__ ids,

@@ -5,14 +5,17 @@
 //     dist_k = max(0, x_sq + c_sq[k] - 2 * <x, c_k>)      (assign_common.cuh:33-36)
 // with the dot product accumulated in fp32 as one fused multiply-add chain in
 // feature order, and the strict-< running minimum that keeps the lowest k on
-// ties (assign_common.cuh:23-28).  It serves fp32 inputs, D % 16 != 0,
-// D > 256 and FKC_ASSIGN_FORCE_SAFE (api.cpp:12-25).
+// ties (assign_common.cuh:23-28).  It serves fp32 inputs, fp16/bf16 with
+// D % 8 != 0 or D > 512, and FKC_ASSIGN_FORCE_SAFE (api.cpp:12-25).
 //
-// Layout: one thread per point, 256 points per workgroup.  Centroids pass
-// through LDS in 32 x 32 (centroid x feature) fp32 tiles; every lane of a
-// wave reads the same LDS word (broadcast), so the tile costs one LDS read
-// per FMA-column and no bank conflicts.  Each thread keeps 32 partial dot
-// products in registers while the feature tiles stream past.
+// Layout: SPLIT adjacent lanes per point (256 / SPLIT points per
+// workgroup); lane s of a point scores centroids k = s (mod SPLIT) of each
+// tile.  Centroids pass through LDS in 32 x 32 (centroid x feature) fp32
+// tiles.  Each lane keeps 32 / SPLIT partial dot products in registers while
+// the feature tiles stream past; every (point, centroid) dot product is one
+// lane's FMA chain in feature order whatever SPLIT is, so labels do not
+// depend on it.  The SPLIT lanes of a point merge with the lowest-index rule
+// at the end.  SPLIT > 1 gives small N enough workgroups to fill the chip.
 #include "device_util.hpp"
 #include "fkc_internal.hpp"
 
@@ -31,7 +34,7 @@ constexpr int VT = 256;   // threads (points) per workgroup
 constexpr int VKC = 32;   // centroids per LDS tile
 constexpr int VDC = 32;   // features per LDS tile
 
-template <int DT>
+template <int DT, int SPLIT>
 __global__ void __launch_bounds__(VT)
 assign_valu_kernel(const typename Elem<DT>::T* __restrict__ x,
                    const typename Elem<DT>::T* __restrict__ c,
@@ -39,13 +42,16 @@ assign_valu_kernel(const typename Elem<DT>::T* __restrict__ x,
                    const float* __restrict__ c_sq, int32_t* __restrict__ ids,
                    int N, int K, int D, const int32_t* __restrict__ ctrl) {
   using E = Elem<DT>;
+  constexpr int PPW = VT / SPLIT;    // points per workgroup
+  constexpr int KPL = VKC / SPLIT;   // centroids per lane per tile
   if (loop_done(ctrl)) return;
-  __shared__ float tile[VKC][VDC];
+  __shared__ float tile[VKC][VDC + 1];
   __shared__ float tile_q[VKC];
 
   const int tid = threadIdx.x;
+  const int sl = tid % SPLIT;        // this lane's centroid residue
   const int b = blockIdx.y;
-  const int n = blockIdx.x * VT + tid;
+  const int n = blockIdx.x * PPW + tid / SPLIT;
   const bool valid = n < N;
   const typename E::T* xr = x + ((size_t)b * N + (valid ? n : 0)) * D;
   const typename E::T* cb = c + (size_t)b * K * D;
@@ -63,9 +69,9 @@ assign_valu_kernel(const typename Elem<DT>::T* __restrict__ x,
   float best = FLT_MAX;
   int bidx = 0;
   for (int k0 = 0; k0 < K; k0 += VKC) {
-    float acc[VKC];
+    float acc[KPL];
 #pragma unroll
-    for (int j = 0; j < VKC; ++j) acc[j] = 0.f;
+    for (int j = 0; j < KPL; ++j) acc[j] = 0.f;
     for (int d0 = 0; d0 < D; d0 += VDC) {
       __syncthreads();
       for (int i = tid; i < VKC * VDC; i += VT) {
@@ -84,31 +90,46 @@ assign_valu_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
         for (int dd = 0; dd < VDC; ++dd) xv[dd] = E::load(xr[d0 + dd]);
 #pragma unroll
-        for (int kk = 0; kk < VKC; ++kk) {
+        for (int j = 0; j < KPL; ++j) {
+          const int kk = j * SPLIT + sl;
 #pragma unroll
           for (int dd = 0; dd < VDC; ++dd)
-            acc[kk] = fmaf(xv[dd], tile[kk][dd], acc[kk]);
+            acc[j] = fmaf(xv[dd], tile[kk][dd], acc[j]);
         }
       } else {
         for (int dd = 0; dd < dn; ++dd) {
           const float xv = E::load(xr[d0 + dd]);
 #pragma unroll
-          for (int kk = 0; kk < VKC; ++kk)
-            acc[kk] = fmaf(xv, tile[kk][dd], acc[kk]);
+          for (int j = 0; j < KPL; ++j)
+            acc[j] = fmaf(xv, tile[j * SPLIT + sl][dd], acc[j]);
         }
       }
     }
-    const int kn = min(VKC, K - k0);
-    for (int kk = 0; kk < kn; ++kk) {
-      float dist = xs + tile_q[kk] - 2.0f * acc[kk];
-      dist = dist > 0.f ? dist : 0.f;
-      if (dist < best) {
-        best = dist;
-        bidx = k0 + kk;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int kk = j * SPLIT + sl;
+      if (k0 + kk < K) {
+        float dist = xs + tile_q[kk] - 2.0f * acc[j];
+        dist = dist > 0.f ? dist : 0.f;
+        if (dist < best) {  // kk rises with j: the first minimum is kept
+          best = dist;
+          bidx = k0 + kk;
+        }
       }
     }
   }
-  if (valid) ids[(size_t)b * N + n] = bidx;
+  // Merge the SPLIT lanes of this point (adjacent lanes): smaller distance,
+  // then smaller index.
+#pragma unroll
+  for (int off = 1; off < SPLIT; off <<= 1) {
+    const float ob = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(bidx, off, 64);
+    if (ob < best || (ob == best && oi < bidx)) {
+      best = ob;
+      bidx = oi;
+    }
+  }
+  if (valid && sl == 0) ids[(size_t)b * N + n] = bidx;
 }
 
 template <int DT>
@@ -131,16 +152,35 @@ row_sqnorm_kernel(const typename Elem<DT>::T* __restrict__ src,
   if (lane == 0) out[row] = acc;
 }
 
+template <int DT, int SPLIT>
+int launch_valu_split(const void* x, const void* c, const float* x_sq,
+                      const float* c_sq, int32_t* ids, int64_t B, int64_t N,
+                      int64_t K, int64_t D, const int32_t* ctrl,
+                      hipStream_t s) {
+  using T = typename Elem<DT>::T;
+  constexpr int PPW = VT / SPLIT;
+  dim3 grid((unsigned)((N + PPW - 1) / PPW), (unsigned)B);
+  hipLaunchKernelGGL((assign_valu_kernel<DT, SPLIT>), grid, dim3(VT), 0, s,
+                     static_cast<const T*>(x), static_cast<const T*>(c), x_sq,
+                     c_sq, ids, (int)N, (int)K, (int)D, ctrl);
+  return check_launch("assign_valu");
+}
+
+// Lanes per point: the smallest power of two (<= 16) that gives the grid at
+// least 1024 workgroups (4 per CU), so small N does not leave CUs idle.
 template <int DT>
 int launch_valu_t(const void* x, const void* c, const float* x_sq,
                   const float* c_sq, int32_t* ids, int64_t B, int64_t N,
                   int64_t K, int64_t D, const int32_t* ctrl, hipStream_t s) {
-  using T = typename Elem<DT>::T;
-  dim3 grid((unsigned)((N + VT - 1) / VT), (unsigned)B);
-  hipLaunchKernelGGL((assign_valu_kernel<DT>), grid, dim3(VT), 0, s,
-                     static_cast<const T*>(x), static_cast<const T*>(c), x_sq,
-                     c_sq, ids, (int)N, (int)K, (int)D, ctrl);
-  return check_launch("assign_valu");
+  int split = 1;
+  while (split < 16 && B * ((N * split + VT - 1) / VT) < 1024) split <<= 1;
+  switch (split) {
+    case 1: return launch_valu_split<DT, 1>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+    case 2: return launch_valu_split<DT, 2>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+    case 4: return launch_valu_split<DT, 4>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+    case 8: return launch_valu_split<DT, 8>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+    default: return launch_valu_split<DT, 16>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+  }
 }
 
 template <int DT>

@@ -241,6 +241,30 @@ int fkc_centroid_finalize(const float* sums, const int32_t* counts,
 }
 
 
+size_t fkc_quality_workspace_bytes(int64_t B, int64_t N, int64_t K) {
+  if (B <= 0 || N < 0 || K < 1) return 0;
+  return quality_workspace_bytes(B, N, K);
+}
+
+int fkc_assigned_inertia(const void* x, const void* centroids,
+                         const int32_t* cluster_ids, int64_t B, int64_t N,
+                         int64_t K, int64_t D, int dtype, double* inertia,
+                         int32_t* empty_clusters, void* workspace,
+                         size_t workspace_bytes, fkc_stream_t stream) {
+  g_err[0] = 0;
+  if (int rc = shape_ok(B, N, K, D, "assigned_inertia")) return rc;
+  if (int rc = dtype_ok(dtype, "assigned_inertia")) return rc;
+  if (B == 0 || (!inertia && !empty_clusters)) return FKC_OK;
+  if (N > 0 && !cluster_ids)
+    return fail(FKC_ERR_INVALID, "assigned_inertia: null cluster_ids");
+  if (inertia && N > 0 && (!x || !centroids))
+    return fail(FKC_ERR_INVALID,
+                "assigned_inertia: x and centroids are needed for inertia");
+  return launch_quality(x, centroids, cluster_ids, B, N, K, D, dtype, inertia,
+                        empty_clusters, workspace, workspace_bytes,
+                        reinterpret_cast<hipStream_t>(stream));
+}
+
 size_t fkc_kmeans_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,
                                   int dtype, int max_iters) {
   if (B <= 0 || N <= 0 || K < 1 || D < 1) return 256;

@@ -92,6 +92,14 @@ int launch_converge_check(const float* shift, int it, float tol, int32_t* ctrl,
 
 // FKC_ASSIGN_FORCE_SAFE=1|true: route every dtype to the fp32 VALU kernel.
 bool force_safe_assign();
+// ---------------------------------------------------------------- quality
+size_t quality_workspace_bytes(int64_t B, int64_t N, int64_t K);
+// inertia (B doubles) and empty (B ints) are device pointers, either NULL.
+int launch_quality(const void* x, const void* c, const int32_t* ids,
+                   int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
+                   double* inertia, int32_t* empty, void* ws, size_t ws_bytes,
+                   hipStream_t s);
+
 // FKC_NTILES=1|2|4: 16-point tiles per wave in the MFMA kernel; 0 = auto.
 int ntiles_override();
 

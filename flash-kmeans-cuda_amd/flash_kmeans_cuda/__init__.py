@@ -9,6 +9,7 @@ the C ABI of include/fkc.h.  Importing fails if the HIP library is missing.
 from ._version import __version__
 from .kmeans import batch_kmeans_Euclid
 from .ops import centroid_finalize, centroid_update_sorted, euclid_assign, label_sort
+from . import quality
 
 __all__ = [
     "__version__",
@@ -17,4 +18,5 @@ __all__ = [
     "centroid_update_sorted",
     "centroid_finalize",
     "label_sort",
+    "quality",
 ]

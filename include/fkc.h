@@ -23,6 +23,7 @@
  *   flash_kmeans_cuda/csrc/bindings.cpp:107-127        (_C extension module)
  *   flash_kmeans_cuda/kmeans.py:108-195                (Lloyd driver loop)
  *   flash_kmeans_cuda/ops.py:58-112                    (torch.sort call site)
+ *   benchmarks/quality_compare.py:69-90                (inertia evaluator)
  */
 #ifndef FKC_H_
 #define FKC_H_
@@ -129,6 +130,26 @@ FKC_CAPI int fkc_centroid_finalize(const float* sums, const int32_t* counts,
                                    const void* old_centroids, void* out,
                                    int64_t B, int64_t K, int64_t D, int dtype,
                                    fkc_stream_t stream);
+
+/*
+ * Clustering quality of labelled points, on the device (the evaluator of the
+ * reference's benchmarks/quality_compare.py:69-90, `_assigned_inertia` and
+ * `_empty_clusters`):
+ *   inertia[b] = sum_n sum_d (float(x[b,n,d]) - float(c[b,ids[b,n],d]))^2,
+ *                difference and square in fp32, sum in fp64;
+ *   empty_clusters[b] = number of k in [0,K) that no point of row b carries.
+ * Rows labelled outside [0,K) add nothing and are not counted.  inertia (B
+ * doubles) and empty_clusters (B int32) are device pointers; either may be
+ * NULL (x and centroids may then be NULL too when inertia is).  The result
+ * is bitwise reproducible (fixed summation order).
+ */
+FKC_CAPI size_t fkc_quality_workspace_bytes(int64_t B, int64_t N, int64_t K);
+FKC_CAPI int fkc_assigned_inertia(const void* x, const void* centroids,
+                                  const int32_t* cluster_ids, int64_t B,
+                                  int64_t N, int64_t K, int64_t D, int dtype,
+                                  double* inertia, int32_t* empty_clusters,
+                                  void* workspace, size_t workspace_bytes,
+                                  fkc_stream_t stream);
 
 /*
  * Whole Lloyd loop of batch_kmeans_Euclid (kmeans.py:108-195) in one call.

@@ -15,6 +15,8 @@ Reference (OpsiClear/flash-kmeans-cuda) semantics restated here:
               (runs of equal sorted labels; labels outside [0,K) skipped)
   finalize    ops.py:115-130, csrc/update/update_finalize.cu:39-66
   loop        flash_kmeans_cuda/kmeans.py:73-195
+  quality     benchmarks/quality_compare.py:69-90 (assigned inertia with
+              fp32 differences and squares summed in fp64; empty clusters)
 
 Arithmetic choices (documented, not the reference's exact rounding):
   * assign ranks exact squared distances: x_sq + c_sq - 2<x,c> evaluated in
@@ -228,3 +230,33 @@ def kmeans(x: np.ndarray, K: int, max_iters: int, tol: float, init: np.ndarray,
             break
         cur = new
     return ids, cur, n
+
+
+def assigned_inertia(x: np.ndarray, ids: np.ndarray, c: np.ndarray, dtype: str) -> np.ndarray:
+    """Per batch row: sum over points and features of (x - c[id])^2, the
+    difference and the square in float32, the total in float64
+    (quality_compare.py:69-83, `diff.square().sum(dtype=torch.float64)`).
+    Rows labelled outside [0,K) add nothing."""
+    xf = to_f32(x, dtype)
+    cf = to_f32(c, dtype)
+    B, N, D = xf.shape
+    K = cf.shape[1]
+    out = np.zeros(B, dtype=np.float64)
+    for b in range(B):
+        ib = np.asarray(ids[b]).astype(np.int64)
+        ok = (ib >= 0) & (ib < K)
+        diff = (xf[b][ok] - cf[b][ib[ok]]).astype(np.float32)
+        sq = (diff * diff).astype(np.float32)
+        out[b] = sq.astype(np.float64).sum()
+    return out
+
+
+def empty_clusters(ids: np.ndarray, K: int) -> np.ndarray:
+    """Per batch row: number of k in [0,K) that no point carries
+    (quality_compare.py:86-88, bincount == 0)."""
+    out = []
+    for b in range(ids.shape[0]):
+        ib = np.asarray(ids[b]).astype(np.int64)
+        ib = ib[(ib >= 0) & (ib < K)]
+        out.append(int((np.bincount(ib, minlength=K) == 0).sum()))
+    return np.asarray(out, dtype=np.int64)

@@ -91,3 +91,21 @@ def lloyd(x, c, iters):
         sums, counts = accumulate(x, labels, len(c), D)
         c = [[s / n for s in sums[k]] if n > 0 else c[k] for k, n in enumerate(counts)]
     return labels, c
+
+
+def assigned_inertia(x_rows, ids, cents, K):
+    """sum over rows of sum_d f32(f32(x - c)^2), total as a Python float;
+    rows labelled outside [0,K) are skipped."""
+    tot = 0.0
+    for row, k in zip(x_rows, ids):
+        if not 0 <= k < K:
+            continue
+        for a, c in zip(row, cents[k]):
+            d = f32(f32(a) - f32(c))
+            tot += f32(d * d)
+    return tot
+
+
+def empty_clusters(ids, K):
+    seen = set(k for k in ids if 0 <= k < K)
+    return sum(1 for k in range(K) if k not in seen)

@@ -29,6 +29,7 @@ def test_header_declares_the_expected_surface():
               "fkc_label_sort_workspace_bytes", "fkc_centroid_update_sorted",
               "fkc_centroid_update_sorted_indexed", "fkc_update_workspace_bytes",
               "fkc_centroid_finalize", "fkc_kmeans_lloyd", "fkc_kmeans_workspace_bytes",
+              "fkc_assigned_inertia", "fkc_quality_workspace_bytes",
               "fkc_last_error", "fkc_version"]:
         assert n in names
 
@@ -90,6 +91,25 @@ def test_invalid_arguments_are_rejected_without_a_device():
     rc, msg = _err(L.fkc_kmeans_lloyd(fake, fake, fake, 1, 100, 4, 8, 1, 3, 0.0, odd,
                                       1 << 24, None, None, None))
     assert rc == 2 and "aligned" in msg
+    # quality evaluator: null labels, missing x for inertia, bad dtype,
+    # small or misaligned workspace, all refused before any launch
+    rc, msg = _err(L.fkc_assigned_inertia(fake, fake, None, 1, 10, 4, 8, 1, fake, fake,
+                                          fake, 1 << 20, None))
+    assert rc == 1 and "cluster_ids" in msg
+    rc, msg = _err(L.fkc_assigned_inertia(None, fake, fake, 1, 10, 4, 8, 1, fake, None,
+                                          fake, 1 << 20, None))
+    assert rc == 1 and "inertia" in msg
+    rc, msg = _err(L.fkc_assigned_inertia(fake, fake, fake, 1, 10, 4, 8, 9, fake, fake,
+                                          fake, 1 << 20, None))
+    assert rc == 1 and "dtype" in msg
+    rc, msg = _err(L.fkc_assigned_inertia(fake, fake, fake, 1, 10, 4, 8, 1, fake, fake,
+                                          fake, 8, None))
+    assert rc == 2 and "workspace" in msg
+    rc, msg = _err(L.fkc_assigned_inertia(fake, fake, fake, 1, 10, 4, 8, 1, fake, fake,
+                                          odd, 1 << 20, None))
+    assert rc == 2 and "aligned" in msg
+    assert L.fkc_assigned_inertia(fake, fake, fake, 1, 10, 4, 8, 1, None, None,
+                                  None, 0, None) == 0  # nothing asked
 
 
 def test_empty_inputs_are_no_ops():

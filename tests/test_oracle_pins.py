@@ -419,3 +419,86 @@ def test_loop_oracle_pinned():
                                     _mut_empty_to_zero])
 def test_loop_battery_rejects_planted_mistakes(mutant):
     assert _loop_battery(mutant) != []
+
+
+# ==================================================================== quality
+def _quality_battery(inertia_fn, empty_fn):
+    fails = []
+    rng = _rng(11)
+    # 1. brute force (float32 difference and square, float64 total)
+    for dtype in ("f32", "f16", "bf16"):
+        B, N, K, D = 2, 37, 6, 5
+        x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32) * 3, dtype)
+        c = O.from_f32(rng.standard_normal((B, K, D)).astype(np.float32) * 3, dtype)
+        ids = rng.integers(-1, K + 1, (B, N)).astype(np.int32)  # some invalid
+        got = inertia_fn(x, ids, c, dtype)
+        xf, cf = O.to_f32(x, dtype), O.to_f32(c, dtype)
+        for b in range(B):
+            want = brute.assigned_inertia(_as_lists(xf[b]), list(map(int, ids[b])),
+                                          _as_lists(cf[b]), K)
+            if not np.isclose(got[b], want, rtol=1e-13, atol=0):
+                fails.append(f"brute {dtype} b={b}: {got[b]!r} vs {want!r}")
+        e = empty_fn(ids, K)
+        for b in range(B):
+            if e[b] != brute.empty_clusters(list(map(int, ids[b])), K):
+                fails.append(f"empty {dtype} b={b}")
+    # 2. library: with labels from scipy's vq, inertia = sum of vq distances^2
+    from scipy.cluster.vq import vq
+    x = rng.standard_normal((1, 500, 16)).astype(np.float32)
+    c = rng.standard_normal((1, 40, 16)).astype(np.float32)
+    lab, dist = vq(x[0].astype(np.float64), c[0].astype(np.float64))
+    got = inertia_fn(x, lab[None].astype(np.int32), c, "f32")
+    if not np.isclose(got[0], (dist ** 2).sum(), rtol=1e-6):
+        fails.append("scipy vq distances")
+    # 3. known answers: labels at the centroids themselves give zero;
+    # a point at distance 3 from its centroid gives 9
+    c = np.zeros((1, 3, 4), np.float32)
+    c[0, 1, 0] = 5.0
+    x = np.zeros((1, 2, 4), np.float32)
+    x[0, 0, 0] = 5.0
+    x[0, 1, 2] = 3.0
+    got = inertia_fn(x, np.array([[1, 0]], np.int32), c, "f32")
+    if got[0] != 9.0:
+        fails.append(f"known answer {got[0]}")
+    if empty_fn(np.array([[1, 0, 1]], np.int32), 3)[0] != 1:
+        fails.append("known empty count")
+    return fails
+
+
+def _mut_f64_square(x, ids, c, dtype):
+    xf, cf = O.to_f64(x, dtype), O.to_f64(c, dtype)
+    out = []
+    for b in range(xf.shape[0]):
+        ok = (ids[b] >= 0) & (ids[b] < cf.shape[1])
+        out.append(((xf[b][ok] - cf[b][ids[b][ok]]) ** 2).sum())
+    return np.asarray(out)
+
+
+def _mut_clip_invalid(x, ids, c, dtype):
+    return O.assigned_inertia(x, np.clip(ids, 0, c.shape[1] - 1), c, dtype)
+
+
+def _mut_norm_not_squared(x, ids, c, dtype):
+    xf, cf = O.to_f32(x, dtype), O.to_f32(c, dtype)
+    out = []
+    for b in range(xf.shape[0]):
+        ok = (ids[b] >= 0) & (ids[b] < cf.shape[1])
+        out.append(np.linalg.norm(xf[b][ok] - cf[b][ids[b][ok]], axis=1).astype(np.float64).sum())
+    return np.asarray(out)
+
+
+def _mut_empty_off_by_one(ids, K):
+    return O.empty_clusters(ids, K) - (ids == K - 1).any(axis=1)
+
+
+def test_quality_oracle_pinned():
+    assert _quality_battery(O.assigned_inertia, O.empty_clusters) == []
+
+
+@pytest.mark.parametrize("mutant", [_mut_f64_square, _mut_clip_invalid, _mut_norm_not_squared])
+def test_quality_battery_rejects_planted_inertia_mistakes(mutant):
+    assert _quality_battery(mutant, O.empty_clusters) != []
+
+
+def test_quality_battery_rejects_planted_empty_count_mistake():
+    assert _quality_battery(O.assigned_inertia, _mut_empty_off_by_one) != []
