@@ -74,6 +74,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #ifndef FKC_SCHED_GROUPS
 #define FKC_SCHED_GROUPS 1
 #endif
+#ifndef FKC_SG_LEAD
+#define FKC_SG_LEAD 1
+#endif
+#ifndef FKC_SG_VALU
+#define FKC_SG_VALU 1
+#endif
 
 constexpr int KC = 64;  // centroid rows per register-staged LDS stage
 constexpr int THREADS = 256;  // 4 waves
@@ -204,16 +210,21 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // sixteen rows a fragment read touches then fall on distinct banks.  The
     // two stage buffers are separate arrays, so the compiler can tell that
     // loads into one do not alias reads from the other and need not wait
-    // for them.  Each lane's source offset within a stage is fixed, so a
-    // stage costs one scalar address update; only the last, partial stage
-    // clamps rows to K-1.  c_sq lands raw and each wave scales (and masks
-    // past K) its own share once its loads are in, before the barrier.
+    // for them.  Each lane's source offset within a stage is fixed and the
+    // stage base is wave-uniform, so a stage's loads cost no vector ALU
+    // work.  With K >= KCD no row is clamped: the last stage starts at
+    // K - KCD instead, re-scoring rows an earlier stage saw (a re-seen row
+    // can never beat its own earlier score, so the first-maximum rule still
+    // holds, and every candidate row stays below K).  Only K < KCD clamps
+    // rows to K-1.  c_sq lands raw and each wave scales (and masks past K)
+    // its own share once its loads are in, before the barrier.
     constexpr int KCD = DS2 <= 4 ? FKC_KC_DMA : 64;
     constexpr int ROWB = DP * 2;
     constexpr int STAGE = KCD * ROWB;
     constexpr int LOADS = STAGE / (THREADS * 16);
     constexpr int QW = KCD / 4;  // c_sq entries loaded per wave
     static_assert(STAGE % (THREADS * 16) == 0 && QW <= 64, "stage split");
+    static_assert((ROWB & (ROWB - 1)) == 0, "power-of-two stage rows");
     __shared__ __attribute__((aligned(1024))) uint8_t s_c0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t s_c1[STAGE];
     __shared__ __attribute__((aligned(256))) float s_q0[KCD];
@@ -221,38 +232,50 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     typedef __attribute__((address_space(1))) void gvoid;
     typedef __attribute__((address_space(3))) void lvoid;
 
-    static_assert((ROWB & (ROWB - 1)) == 0, "power-of-two stage rows");
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);  // scalar copy
     // Source byte of load j within a stage: row * ROWB + permuted segment.
-    // Recomputed per stage (a few VALU ops) rather than held in registers.
     auto soff = [&](int j) {
-      const int pos = (wave * LOADS + j) * 1024 + lane * 16;
+      const int pos = (uwave * LOADS + j) * 1024 + lane * 16;
       const int r = pos / ROWB, v = (pos % ROWB) / 16;
       return (uint32_t)(r * ROWB + (v ^ swz<SEGS>(r)) * 16);
     };
-    const int qi = wave * QW + lane;  // this lane's c_sq slot (lane < QW)
-    const int sw = swz<SEGS>(col);    // rows 16t + col share it
+    uint32_t so[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) so[j] = soff(j);
+    const int qi = uwave * QW + lane;  // this lane's c_sq slot (lane < QW)
+    const int sw = swz<SEGS>(col);     // rows 16t + col share it
     const int nch = (K + KCD - 1) / KCD;
+    const bool overlap = K >= KCD;     // wave-uniform
     const char* cbase = reinterpret_cast<const char*>(cb);
+    auto kbase = [&](int chunk) {
+      return overlap ? min(chunk * KCD, K - KCD) : 0;
+    };
 
     auto issue = [&](int chunk, uint8_t* dc, float* dq) {
-      const int kb = chunk * KCD;
+      const int kb = kbase(chunk);
       const char* src = cbase + (size_t)kb * ROWB;
-      const bool tail = kb + KCD > K;
+      if (overlap) {
 #pragma unroll
-      for (int j = 0; j < LOADS; ++j) {
-        uint32_t off = soff(j);
-        if (tail) {
-          const int r = (int)(off / ROWB);
-          off = (uint32_t)(min(r, K - 1 - kb) * ROWB) + off % ROWB;
+        for (int j = 0; j < LOADS; ++j)
+          __builtin_amdgcn_global_load_lds(
+              (gvoid*)(src + so[j]), (lvoid*)(dc + (uwave * LOADS + j) * 1024),
+              16, 0, 0);
+        if (lane < QW)
+          __builtin_amdgcn_global_load_lds((gvoid*)(qb + kb + qi),
+                                           (lvoid*)(dq + uwave * QW), 4, 0, 0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+          const int r = (int)(so[j] / ROWB);
+          const uint32_t off =
+              (uint32_t)(min(r, K - 1) * ROWB) + so[j] % ROWB;
+          __builtin_amdgcn_global_load_lds(
+              (gvoid*)(src + off), (lvoid*)(dc + (uwave * LOADS + j) * 1024),
+              16, 0, 0);
         }
-        __builtin_amdgcn_global_load_lds(
-            (gvoid*)(src + off), (lvoid*)(dc + (wave * LOADS + j) * 1024), 16,
-            0, 0);
-      }
-      if (lane < QW) {
-        const uint32_t k = (uint32_t)min(qi, K - 1 - kb);
-        __builtin_amdgcn_global_load_lds((gvoid*)(qb + kb + k),
-                                         (lvoid*)(dq + wave * QW), 4, 0, 0);
+        if (lane < QW)
+          __builtin_amdgcn_global_load_lds((gvoid*)(qb + min(qi, K - 1)),
+                                           (lvoid*)(dq + uwave * QW), 4, 0, 0);
       }
     };
     // After this wave's loads have landed: scale its c_sq share in place.
@@ -260,9 +283,9 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // value), so no block boundary splits the stage's code: a boundary here
     // lets the compiler sink the stage's folds below it, away from the
     // matrix-core work they should overlap.
-    const int qf = wave * QW + (lane % QW);
+    const int qf = uwave * QW + (lane % QW);
     auto fixq = [&](int chunk, float* dq) {
-      const int k = chunk * KCD + qf;
+      const int k = kbase(chunk) + qf;
       const float v = dq[qf];
       dq[qf] = k < K ? -0.5f * v : -INFINITY;
     };
@@ -282,7 +305,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // serialises the two units within a wave (measured: 0.86 -> 0.81 ms at
     // N=524288, K=8192, D=128; with fewer tiles the groups cost time).
     auto compute = [&](int chunk, const uint8_t* lc, const float* lq) {
-      const int kb = chunk * KCD;
+      const int kb = kbase(chunk);
       constexpr int NTD = KCD / 16;
       if constexpr (EXACT) {
         // Small K: few stages, so no pipelining; blocks wholly past K (a
@@ -318,10 +341,14 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
           }
           if (t > 0) fold(prev, kb + 16 * (t - 1));
           if constexpr (FKC_SCHED_GROUPS && PT >= 4) {
+            // FKC_SG_LEAD MFMAs first (distance from the previous block's
+            // last MFMA to the first fold op that reads it), then one
+            // MFMA per FKC_SG_VALU vector ops.
 #pragma unroll
             for (int i = 0; i < DS2 * PT; ++i) {
               __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-              __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+              if (i + 1 >= FKC_SG_LEAD)
+                __builtin_amdgcn_sched_group_barrier(0x002, FKC_SG_VALU, 0);
             }
           }
 #pragma unroll
