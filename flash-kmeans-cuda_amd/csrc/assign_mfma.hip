@@ -35,9 +35,10 @@
 // Workgroup: 4 waves x PT point tiles x 16 points (PT chosen per grid size).
 // Centroids pass through LDS in double-buffered stages with one barrier per
 // stage; the next stage's loads are in flight while the matrix cores work
-// on the current one.  For D = 128 / 256 the stages are direct global->LDS
-// loads into unpadded, XOR-permuted rows (no staging registers, no bank
-// conflicts); other widths stage through VGPRs into rows padded by 16 bytes.
+// on the current one.  For D = 32, 64, 128 and 256 the stages are direct
+// global->LDS loads into unpadded, XOR-permuted rows (no staging registers,
+// no bank conflicts); other widths stage through VGPRs into rows padded by
+// 16 bytes.
 // Centroid rows past K re-read row K-1 instead of branching (their scores
 // are masked to -inf).
 #include "device_util.hpp"
@@ -155,9 +156,10 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
   constexpr int PTS_WG = 4 * PTS_WAVE;
   constexpr int NT = KC / 16;
 
-  // Direct-to-LDS stages measured faster for D = 128 and 256 only (at D = 64
-  // the short stages leave their latency exposed).
-  constexpr bool DMA = FKC_USE_DMA && !PAD && (DS2 == 4 || DS2 == 8);
+  // Direct-to-LDS stages for unpadded power-of-two step counts (D = 32, 64,
+  // 128, 256); measured faster than register staging at D = 64 and 128.
+  constexpr bool DMA =
+      FKC_USE_DMA && !PAD && (DS2 == 1 || DS2 == 2 || DS2 == 4 || DS2 == 8);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;

@@ -9,7 +9,8 @@
 // one writer and rows are summed in sorted order, so results are bitwise
 // reproducible:
 //
-//   update_runs  : one wave per unit of 128 consecutive sorted rows.  Lanes
+//   update_runs  : one wave per unit of 128 consecutive sorted rows (64 or
+//                  32 when N is small, for parallelism).  Lanes
 //                  own column slices (64 lanes x VEC x NI columns per pass
 //                  over the row), so every row is one coalesced load per
 //                  lane slice; a unit's labels and permutation entries are
@@ -46,7 +47,15 @@
 namespace fkc {
 namespace {
 
-constexpr int UR = 128;  // sorted rows per unit (one wave)
+constexpr int UR_MAX = 128;  // sorted rows per unit (one wave), at most
+
+// Rows per unit: 128 when that still gives >= 2048 units (512 workgroups),
+// else 64, else 32 — small N needs the extra waves to hide its latency.
+int choose_ur(int64_t B, int64_t N) {
+  for (int ur = UR_MAX; ur > 32; ur >>= 1)
+    if (B * ((N + ur - 1) / ur) >= 2048) return ur;
+  return 32;
+}
 constexpr int UT = 256;  // threads per workgroup: 4 units
 constexpr int UB = 64;   // units per block of the two-level run merge
 
@@ -98,7 +107,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
                    const int32_t* __restrict__ sids, float* __restrict__ sums,
                    int32_t* __restrict__ counts, float* __restrict__ part,
                    int32_t* __restrict__ meta, int N, int K, int D,
-                   int nunits, int overwrite,
+                   int nunits, int ur, int overwrite,
                    const int32_t* __restrict__ ctrl) {
   using T = typename Elem<DT>::T;
   constexpr int RB = 32 / NI;  // rows in flight per wave
@@ -109,8 +118,8 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   if (u >= nunits) return;
   const bool lead = blockIdx.z == 0;  // column block 0 writes counts / meta
   const int cbase = blockIdx.z * (64 * VEC * NI);
-  const int p0 = u * UR;
-  const int p1 = min(p0 + UR, N);
+  const int p0 = u * ur;
+  const int p1 = min(p0 + ur, N);
 
   const int32_t* ib = sids + (size_t)b * N;
   const int32_t* pb = INDEXED ? perm + (size_t)b * N : nullptr;
@@ -201,7 +210,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
 
   // Labels and permutation entries of the unit's rows, one per lane per
   // 64-row chunk, loaded up front.
-  constexpr int CH = UR / 64;
+  constexpr int CH = UR_MAX / 64;
   int ivs[CH], pvs[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -474,13 +483,14 @@ int launch_runs_t(const void* x, const int32_t* perm, const int32_t* sids,
                   int64_t B, int64_t N, int64_t K, int64_t D, int64_t nunits,
                   bool overwrite, const int32_t* ctrl, hipStream_t s) {
   using T = typename Elem<DT>::T;
+  const int ur = choose_ur(B, N);
   const int64_t cols_per_block = 64 * VEC * NI;
   dim3 grid((unsigned)((nunits + 3) / 4), (unsigned)B,
             (unsigned)((D + cols_per_block - 1) / cols_per_block));
   hipLaunchKernelGGL((update_runs_kernel<DT, VEC, NI, INDEXED>), grid,
                      dim3(UT), 0, s, static_cast<const T*>(x), perm, sids,
                      sums, counts, part, meta, (int)N, (int)K, (int)D,
-                     (int)nunits, overwrite ? 1 : 0, ctrl);
+                     (int)nunits, ur, overwrite ? 1 : 0, ctrl);
   return check_launch("update_runs");
 }
 
@@ -509,7 +519,8 @@ int launch_runs_dt(const void* x, const int32_t* perm, const int32_t* sids,
 }  // namespace
 
 size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D) {
-  const int64_t nunits = (N + UR - 1) / UR;
+  const int ur = choose_ur(B, N);
+  const int64_t nunits = (N + ur - 1) / ur;
   const int64_t nblocks = (nunits + UB - 1) / UB;
   Carve c(nullptr);
   c.take<float>((size_t)B * nunits * 2 * D);     // unit head/tail partials
@@ -538,7 +549,8 @@ int launch_update(const void* x, const int32_t* perm,
     return fail(FKC_ERR_WORKSPACE,
                 "centroid_update: workspace not %d-byte aligned",
                 kWorkspaceAlign);
-  const int64_t nunits = (N + UR - 1) / UR;
+  const int ur = choose_ur(B, N);
+  const int64_t nunits = (N + ur - 1) / ur;
   Carve c(ws);
   const int64_t nblocks = (nunits + UB - 1) / UB;
   float* part = c.take<float>((size_t)B * nunits * 2 * D);
