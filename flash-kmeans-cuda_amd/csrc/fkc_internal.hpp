@@ -53,10 +53,11 @@ struct SortPlan {
   int bits[4] = {0};    // digit width of each pass
   int shift[4] = {0};   // bit offset of each pass
   int64_t ntiles = 0;   // key tiles per batch row
+  int tile = 4096;      // keys per tile
 };
 // labels_valid: the caller guarantees every label is in [0,K), which saves
 // the sentinel bin (K = 256 then sorts in one 8-bit pass).
-SortPlan sort_plan(int64_t N, int64_t K, bool labels_valid);
+SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid);
 size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K);
 int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
                       int64_t B, int64_t N, int64_t K, bool labels_valid,

@@ -8,12 +8,14 @@
 // caller vouches that every label is valid (labels straight from the assign
 // kernel), split into passes of at most 8 bits.
 // Each pass is reduce-then-scan, with no inter-workgroup waiting:
-//   sort_hist    : per 4096-key tile, a digit histogram in LDS, written
-//                  digit-major to hist[b][digit][tile];
+//   sort_hist    : per tile of 4096 keys (1024 for small N), a digit
+//                  histogram in LDS, written digit-major to
+//                  hist[b][digit][tile];
 //   sort_scan    : exclusive scan of hist[b] (digit-major, so the scan gives
 //                  every (digit, tile) its global output offset);
-//   sort_scatter : each of 8 waves ranks its 512 keys (8 chunks of 64)
-//                  stably: a ballot per digit bit yields, for every lane, the
+//   sort_scatter : each wave ranks its share of the tile (8 waves x 512
+//                  keys, or 4 waves x 256 keys for 1024-key tiles) stably,
+//                  64 keys at a time: a ballot per digit bit yields, for every lane, the
 //                  mask of lanes holding the same digit ("multi-split"); its
 //                  rank is the per-wave digit counter plus the matching lanes
 //                  below it.  Keys are placed in LDS in tile-sorted order,
@@ -27,12 +29,19 @@
 namespace fkc {
 namespace {
 
-constexpr int TILE = 4096;        // keys per tile (one workgroup)
 constexpr int HT = 256;           // threads of the histogram kernel
-constexpr int ST = 512;           // threads of the scatter kernel
-constexpr int SW = ST / 64;       // scatter waves
-constexpr int PER_WAVE = TILE / SW;
-constexpr int CHUNKS = PER_WAVE / 64;
+
+// Keys per tile (one workgroup of each kernel): 4096, or 1024 for small N so
+// that the grid still has some width.
+template <int TILE_>
+struct Geom {
+  static constexpr int TILE = TILE_;
+  static constexpr int ST = TILE_ >= 4096 ? 512 : 256;  // scatter threads
+  static constexpr int SW = ST / 64;                    // scatter waves
+  static constexpr int PER_WAVE = TILE / SW;
+  static constexpr int CHUNKS = PER_WAVE / 64;
+  static_assert(ST >= 256 && CHUNKS >= 1, "scatter geometry");
+};
 
 __device__ inline uint32_t sort_key(int32_t id, int K) {
   return (uint32_t)id < (uint32_t)K ? (uint32_t)id : (uint32_t)K;
@@ -42,6 +51,7 @@ __device__ inline uint32_t sort_key(int32_t id, int K) {
 // rounded to whole int4s so every batch row starts 16-byte aligned.
 inline int64_t table_stride(int64_t ntiles) { return (256 * ntiles + 3) / 4 * 4; }
 
+template <int TILE>
 __global__ void __launch_bounds__(HT)
 sort_hist_kernel(const int32_t* __restrict__ keys, int32_t* __restrict__ hist,
                  int N, int K, int shift, int bits, int ntiles, int64_t hstride,
@@ -124,6 +134,7 @@ sort_scan_kernel(int32_t* __restrict__ hist, int64_t len, int64_t hstride,
 // Stable rank of every key of one tile by its digit, then a coalesced
 // write-out: keys are first placed in LDS in tile-sorted order, then each
 // digit's contiguous run is copied to its global slot.
+template <int TILE, int ST = Geom<TILE>::ST>
 __global__ void __launch_bounds__(ST)
 sort_scatter_kernel(const int32_t* __restrict__ keys_in,
                     const int32_t* __restrict__ vals_in,
@@ -132,6 +143,9 @@ sort_scatter_kernel(const int32_t* __restrict__ keys_in,
                     const int32_t* __restrict__ offs, int N, int K, int shift,
                     int bits, int ntiles, int64_t hstride,
                     const int32_t* __restrict__ ctrl) {
+  constexpr int SW = Geom<TILE>::SW;
+  constexpr int PER_WAVE = Geom<TILE>::PER_WAVE;
+  constexpr int CHUNKS = Geom<TILE>::CHUNKS;
   if (loop_done(ctrl)) return;
   __shared__ int cnt[SW][256];
   __shared__ int dstart[256];
@@ -225,7 +239,7 @@ sort_scatter_kernel(const int32_t* __restrict__ keys_in,
 
 }  // namespace
 
-SortPlan sort_plan(int64_t N, int64_t K, bool labels_valid) {
+SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
   SortPlan p;
   const int64_t span = labels_valid ? K : K + 1;  // K + 1: room for sentinel K
   int bits = 0;
@@ -239,12 +253,16 @@ SortPlan sort_plan(int64_t N, int64_t K, bool labels_valid) {
     p.shift[i] = shift;
     shift += w;
   }
-  p.ntiles = (N + TILE - 1) / TILE;
+  // 1024-key tiles widen the grid for small N; past 128 tiles per batch row
+  // the single-workgroup scan of the (256 x tiles) table costs more than the
+  // extra width saves (measured: N = 131072 gains, N = 524288 loses).
+  p.tile = N <= 131072 ? 1024 : 4096;
+  p.ntiles = (N + p.tile - 1) / p.tile;
   return p;
 }
 
 size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K) {
-  const SortPlan p = sort_plan(N, K, false);  // the larger of the two plans
+  const SortPlan p = sort_plan(B, N, K, false);  // the larger of the two plans
   Carve c(nullptr);
   c.take<int32_t>((size_t)B * table_stride(p.ntiles));  // digit table
   const int tmp = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
@@ -267,7 +285,7 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
   if (reinterpret_cast<uintptr_t>(ws) % kWorkspaceAlign != 0)
     return fail(FKC_ERR_WORKSPACE, "label_sort: workspace not %d-byte aligned",
                 kWorkspaceAlign);
-  const SortPlan p = sort_plan(N, K, labels_valid);
+  const SortPlan p = sort_plan(B, N, K, labels_valid);
   Carve c(ws);
   const int64_t hstride = table_stride(p.ntiles);
   int32_t* hist = c.take<int32_t>((size_t)B * hstride);
@@ -290,18 +308,28 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
     int32_t* vout = last ? perm : tv[i % 2];
     const int nb = 1 << p.bits[i];
     dim3 grid((unsigned)p.ntiles, (unsigned)B);
-    hipLaunchKernelGGL(sort_hist_kernel, grid, dim3(HT), 0, s, kin, hist,
-                       (int)N, (int)K, p.shift[i], p.bits[i], (int)p.ntiles,
-                       hstride, ctrl);
+    if (p.tile == 4096)
+      hipLaunchKernelGGL(sort_hist_kernel<4096>, grid, dim3(HT), 0, s, kin, hist,
+                         (int)N, (int)K, p.shift[i], p.bits[i], (int)p.ntiles,
+                         hstride, ctrl);
+    else
+      hipLaunchKernelGGL(sort_hist_kernel<1024>, grid, dim3(HT), 0, s, kin, hist,
+                         (int)N, (int)K, p.shift[i], p.bits[i], (int)p.ntiles,
+                         hstride, ctrl);
     int rc = check_launch("sort_hist");
     if (rc) return rc;
     hipLaunchKernelGGL(sort_scan_kernel, dim3((unsigned)B), dim3(1024), 0, s,
                        hist, (int64_t)nb * p.ntiles, hstride, ctrl);
     rc = check_launch("sort_scan");
     if (rc) return rc;
-    hipLaunchKernelGGL(sort_scatter_kernel, grid, dim3(ST), 0, s, kin, vin,
-                       kout, vout, hist, (int)N, (int)K, p.shift[i],
-                       p.bits[i], (int)p.ntiles, hstride, ctrl);
+    if (p.tile == 4096)
+      hipLaunchKernelGGL(sort_scatter_kernel<4096>, grid, dim3(Geom<4096>::ST), 0,
+                         s, kin, vin, kout, vout, hist, (int)N, (int)K,
+                         p.shift[i], p.bits[i], (int)p.ntiles, hstride, ctrl);
+    else
+      hipLaunchKernelGGL(sort_scatter_kernel<1024>, grid, dim3(Geom<1024>::ST), 0,
+                         s, kin, vin, kout, vout, hist, (int)N, (int)K,
+                         p.shift[i], p.bits[i], (int)p.ntiles, hstride, ctrl);
     rc = check_launch("sort_scatter");
     if (rc) return rc;
     kin = kout;
