@@ -5,7 +5,11 @@ Outputs (git-ignored, shipped with the tree to the GPU box):
   flash_kmeans_cuda/libflash_kmeans_cuda.so   libtorch fkc:: API on top of it
   flash_kmeans_cuda/bin/fkc_cpp_smoke         C++ smoke test of the fkc:: API
 
-Usage: python flash-kmeans-cuda_amd/build.py [--only capi|torch|all] [-j N]
+  _cmake/install/                             CMake install/export package
+                                              (cmake --install of CMakeLists.txt)
+  _cmake/consumer/consumer_smoke              C++ consumer built against it
+
+Usage: python flash-kmeans-cuda_amd/build.py [--only capi|torch|cmake|all] [-j N]
 """
 
 from __future__ import annotations
@@ -53,14 +57,14 @@ KERNEL_SOURCES = [
 HOST_SOURCES = ["capi.cpp"]
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str], quiet: bool = False) -> None:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"build step failed ({proc.returncode}):\n"
                            f"{' '.join(cmd)}\n{proc.stdout}\n{err}")
-    if err.strip():
+    if err.strip() and not quiet:
         sys.stderr.write(err + "\n")
 
 
@@ -126,9 +130,35 @@ def build_torch_api() -> list[str]:
     return [lib, exe]
 
 
+CMAKE_DIR = os.path.join(HERE, "_cmake")
+
+
+def build_cmake_package(jobs: int) -> list[str]:
+    """The CMake install/export package (CMakeLists.txt) into _cmake/install,
+    then the installed-package consumer (cpp_tests/consumer) against it."""
+    import torch
+    cmake = shutil.which("cmake")
+    if cmake is None:
+        raise RuntimeError("cmake not found")
+    gen = ["-G", "Ninja"] if shutil.which("ninja") else []
+    prefix = f"{torch.utils.cmake_prefix_path};{ROCM}"
+    bdir = os.path.join(CMAKE_DIR, "build")
+    inst = os.path.join(CMAKE_DIR, "install")
+    cons = os.path.join(CMAKE_DIR, "consumer")
+    # (Torch's CMake config prints warnings on every configure: quiet.)
+    _run([cmake, "-S", HERE, "-B", bdir, *gen, "-DCMAKE_BUILD_TYPE=Release",
+          f"-DCMAKE_PREFIX_PATH={prefix}"], quiet=True)
+    _run([cmake, "--build", bdir, "-j", str(max(1, jobs))], quiet=True)
+    _run([cmake, "--install", bdir, "--prefix", inst], quiet=True)
+    _run([cmake, "-S", os.path.join(HERE, "cpp_tests", "consumer"), "-B", cons, *gen,
+          "-DCMAKE_BUILD_TYPE=Release", f"-DCMAKE_PREFIX_PATH={inst};{prefix}"], quiet=True)
+    _run([cmake, "--build", cons, "-j", str(max(1, jobs))], quiet=True)
+    return [inst, os.path.join(cons, "consumer_smoke")]
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--only", choices=["capi", "torch", "all"], default="all")
+    ap.add_argument("--only", choices=["capi", "torch", "cmake", "all"], default="all")
     ap.add_argument("-j", "--jobs", type=int,
                     default=min(8, os.cpu_count() or 1))
     args = ap.parse_args(argv)
@@ -136,6 +166,9 @@ def main(argv: list[str] | None = None) -> int:
         print(build_capi(args.jobs))
     if args.only in ("torch", "all"):
         for p in build_torch_api():
+            print(p)
+    if args.only in ("cmake", "all"):
+        for p in build_cmake_package(args.jobs):
             print(p)
     return 0
 
