@@ -256,3 +256,48 @@ def test_c5_full_size_properties():
     ref = O.assign(x[:, sub], c_np, "f16")
     nd, bad, worst = near_tie_report(x[:, sub], c_np, "f16", ids2[:, sub], ref)
     assert bad == 0 and nd / sub.size < 2e-3
+
+
+def test_lloyd_iteration_captures_into_a_graph():
+    """fkc_kmeans_lloyd with tol <= 0 and no host count is capture-safe (no
+    allocation, no synchronisation, no memset nodes).  One captured
+    iteration is replayed several times, with eager work and
+    synchronisations between replays, and every replay must equal the eager
+    iteration from the same starting centroids bit for bit."""
+    from flash_kmeans_cuda import _lib, synth
+    L = _lib.lib
+    cfg = synth.CONFIGS["c2"]
+    x_np, init_np = synth.make(cfg, N=16384)
+    x = synth.to_torch(x_np, "f16")
+    B, N, K, D = 1, 16384, cfg.K, cfg.D
+    dt = _lib.dtype_code(x.dtype)
+    ws = _lib.workspace(L.fkc_kmeans_workspace_bytes(B, N, K, D, dt, 1), x.device)
+    cents = synth.to_torch(init_np, "f16").clone()
+    ids = torch.empty((B, N), dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+
+    def one():
+        _lib.check(L.fkc_kmeans_lloyd(x.data_ptr(), cents.data_ptr(), ids.data_ptr(), B, N, K,
+                                      D, dt, 1, 0.0, ws.data_ptr(), ws.numel(),
+                                      s.cuda_stream, None, None), "kmeans_lloyd")
+
+    g = torch.cuda.CUDAGraph()
+    start = cents.clone()
+    with torch.cuda.graph(g, stream=s):
+        one()
+    torch.cuda.synchronize()
+    state = start.clone()
+    for rep in range(4):
+        cents.copy_(state)
+        with torch.cuda.stream(s):
+            one()                      # eager reference from `state`
+        torch.cuda.synchronize()
+        e_c, e_i = cents.clone(), ids.clone()
+        cents.copy_(state)
+        ids.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cents, e_c), f"replay {rep}: centroids"
+        assert torch.equal(ids, e_i), f"replay {rep}: labels"
+        state = e_c
