@@ -327,10 +327,15 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
     if (!rc)
       rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
                              L.sort_ws, L.sort_ws_bytes, ctrl, s);
+    // The update finalizes the centroids itself when D <= 512 (no sums /
+    // counts round trip); otherwise finalize runs as its own kernel.
+    const UpdateFinalize fin{centroids, L.c_sq, check ? L.shift + it : nullptr};
+    bool fused = false;
     if (!rc)
       rc = launch_update(x, L.perm, L.sorted, L.sums, L.counts, B, N, K, D,
-                         dtype, true, L.upd_ws, L.upd_ws_bytes, ctrl, s);
-    if (!rc)
+                         dtype, true, L.upd_ws, L.upd_ws_bytes, ctrl, s, &fin,
+                         &fused);
+    if (!rc && !fused)
       rc = launch_finalize(L.sums, L.counts, centroids, centroids, L.c_sq,
                            check ? L.shift + it : nullptr, B, K, D, dtype, ctrl,
                            s);

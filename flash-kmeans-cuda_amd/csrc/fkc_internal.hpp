@@ -69,11 +69,23 @@ size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D);
 // overwrite=false: sums/counts += run totals (caller zeroed them).
 // overwrite=true : every bin of sums/counts is written (absent bins get 0);
 //                  requires every label in [0,K) and sorted order.
+// Finalize fused into the update (Lloyd loop, overwrite mode): the new
+// centroids are written in place to `cent`, their squared norms to `c_sq`,
+// the max shift to `shift` (may be null), so no sums/counts round trip and
+// no finalize launch are needed.
+struct UpdateFinalize {
+  void* cent;
+  float* c_sq;
+  float* shift;
+};
+// fin: optional fused finalize; *fused (may be null) reports whether it was
+// applied (it needs D <= 512); when not, the caller runs launch_finalize.
 int launch_update(const void* x, const int32_t* perm /*nullable*/,
                   const int32_t* ids_sorted, float* sums, int32_t* counts,
                   int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
                   bool overwrite, void* ws, size_t ws_bytes,
-                  const int32_t* ctrl, hipStream_t s);
+                  const int32_t* ctrl, hipStream_t s,
+                  const UpdateFinalize* fin = nullptr, bool* fused = nullptr);
 
 // ---------------------------------------------------------------- finalize
 // c_sq_out / shift_out may be null.  shift_out receives max over rows of

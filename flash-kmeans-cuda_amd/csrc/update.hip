@@ -100,6 +100,56 @@ struct UnitMeta {  // per unit, int32 x 4
   enum { TAIL_ID = 0, TAIL_LEN = 1, HEAD_LEN = 2, THROUGH = 3 };
 };
 
+constexpr int FIN_DMAX = 512;  // widest row the fused finalize stages in LDS
+
+// Finalize fused into the update (the Lloyd loop): where a bin's final sum
+// is known, the wave that holds it computes the new centroid row at once,
+// exactly as finalize_kernel (finalize.hip) would from the stored sums:
+// new = cast(sum / count) with IEEE division, c_sq = sum of new^2 and the
+// row's shift ||new - old||_2, both accumulated lane-strided (d = lane,
+// lane+64, ...) in fma order and reduced by wave_sum, so every bit matches
+// the separate kernel.  The row's sums come from LDS (`row`).  Empty bins
+// are left alone: their centroid, c_sq and zero shift stand.
+template <typename T>
+struct FinArgs {
+  T* cent;          // (B, K, D) centroids, updated in place; null: not fused
+  float* c_sq;      // (B, K) next iteration's c_sq
+  float* shift;     // this iteration's max shift (float bits), may be null
+};
+
+// The lanes of one wave wrote `row` in LDS; make the writes visible to the
+// wave's own later reads of other lanes' entries (compiler ordering, and
+// LDS counter drained; global loads in flight are not waited for).
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int DT>
+__device__ inline void finalize_row(const float* row, int cnt,
+                                    typename Elem<DT>::T* crow, float* csq,
+                                    float* shift, int D, int lane) {
+  using E = Elem<DT>;
+  const float fc = (float)cnt;
+  float sq = 0.f, sh = 0.f;
+  for (int d = lane; d < D; d += 64) {
+    const typename E::T o = crow[d];
+    const typename E::T n = E::store(row[d] / fc);
+    crow[d] = n;
+    const float nf = E::load(n), df = nf - E::load(o);
+    sq = fmaf(nf, nf, sq);
+    sh = fmaf(df, df, sh);
+  }
+  sq = wave_sum(sq);
+  if (lane == 0) *csq = sq;
+  if (shift != nullptr) {
+    sh = wave_sum(sh);
+    if (lane == 0)
+      atomicMax(reinterpret_cast<unsigned int*>(shift), __float_as_uint(sqrtf(sh)));
+  }
+}
+
 template <int DT, int VEC, int NI, bool INDEXED>
 __global__ void __launch_bounds__(UT)
 update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
@@ -108,9 +158,11 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
                    int32_t* __restrict__ counts, float* __restrict__ part,
                    int32_t* __restrict__ meta, int N, int K, int D,
                    int nunits, int ur, int overwrite,
+                   FinArgs<typename Elem<DT>::T> fin,
                    const int32_t* __restrict__ ctrl) {
   using T = typename Elem<DT>::T;
   constexpr int RB = 32 / NI;  // rows in flight per wave
+  __shared__ float fin_row[UT / 64][FIN_DMAX];
   if (loop_done(ctrl)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.y;
@@ -121,6 +173,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   const int p0 = u * ur;
   const int p1 = min(p0 + ur, N);
 
+  const bool fused = fin.cent != nullptr;  // uniform
   const int32_t* ib = sids + (size_t)b * N;
   const int32_t* pb = INDEXED ? perm + (size_t)b * N : nullptr;
   const T* xb = x + (size_t)b * N * D;
@@ -186,6 +239,17 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
       store_part(1);
       tail_id = id;
       tail_len = e - s;
+    } else if (fused && (uint32_t)id < (uint32_t)K) {
+      float* r = fin_row[wave];
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        if (cok[i]) {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) r[col[i] + v] = acc[i][v];
+        }
+      wave_lds_sync();
+      finalize_row<DT>(r, e - s, fin.cent + ((size_t)b * K + id) * D,
+                       fin.c_sq + (size_t)b * K + id, fin.shift, D, lane);
     } else if ((uint32_t)id < (uint32_t)K) {
       float* dst = sb + (size_t)id * D;
 #pragma unroll
@@ -221,7 +285,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
 
   int cur = __builtin_amdgcn_readfirstlane(ivs[0]);
   int rs = p0;
-  if (overwrite && !(has_prev && prev == cur))
+  if (overwrite && !fused && !(has_prev && prev == cur))
     zero_bins(has_prev ? prev + 1 : 0, cur);
 
   using R = typename RawCols<DT, VEC>::T;
@@ -254,7 +318,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
           const int id = __builtin_amdgcn_readlane(iv, j);
           if (id != cur) {
             flush(cur, rs, base + j);
-            if (overwrite) zero_bins(cur + 1, id);
+            if (overwrite && !fused) zero_bins(cur + 1, id);
             cur = id;
             rs = base + j;
 #pragma unroll
@@ -274,7 +338,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     }
   }
   flush(cur, rs, p1);
-  if (overwrite && !has_next) zero_bins(cur + 1, K);
+  if (overwrite && !fused && !has_next) zero_bins(cur + 1, K);
 
   if (lead && lane == 0) {
     int32_t* m = meta + ((size_t)b * nunits + u) * 4;
@@ -391,6 +455,7 @@ update_blocks_kernel(const float* __restrict__ part,
 }
 
 // One wave per unit; only units holding a tail partial (run owners) work.
+template <int DT>
 __global__ void __launch_bounds__(UT)
 update_merge_kernel(const float* __restrict__ part,
                     const int32_t* __restrict__ meta,
@@ -398,7 +463,9 @@ update_merge_kernel(const float* __restrict__ part,
                     const int32_t* __restrict__ bmeta, float* __restrict__ sums,
                     int32_t* __restrict__ counts, int K, int D, int nunits,
                     int nblocks, int overwrite,
+                    FinArgs<typename Elem<DT>::T> fin,
                     const int32_t* __restrict__ ctrl) {
+  __shared__ float fin_row[UT / 64][FIN_DMAX];
   if (loop_done(ctrl)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.y;
@@ -462,12 +529,20 @@ update_merge_kernel(const float* __restrict__ part,
   }
   const int len = tail_len + wave_sum_i(l);
 
-  float* dst = sums + ((size_t)b * K + id) * D;
+  const bool fused = fin.cent != nullptr;  // uniform
+  float* dst = fused ? fin_row[wave] : sums + ((size_t)b * K + id) * D;
   const float* tail = pb + ((size_t)u * 2 + 1) * D;
+  const int add = (overwrite || fused) ? 0 : 1;
   if (D % 4 == 0)
-    wave_ordered_sum<4>(tail, n, D, row, dst, overwrite ? 0 : 1, lane);
+    wave_ordered_sum<4>(tail, n, D, row, dst, add, lane);
   else
-    wave_ordered_sum<1>(tail, n, D, row, dst, overwrite ? 0 : 1, lane);
+    wave_ordered_sum<1>(tail, n, D, row, dst, add, lane);
+  if (fused) {
+    wave_lds_sync();
+    finalize_row<DT>(fin_row[wave], len, fin.cent + ((size_t)b * K + id) * D,
+                     fin.c_sq + (size_t)b * K + id, fin.shift, D, lane);
+    return;
+  }
   if (lane == 0) {
     int32_t* cp = counts + (size_t)b * K + id;
     if (overwrite)
@@ -477,43 +552,90 @@ update_merge_kernel(const float* __restrict__ part,
   }
 }
 
+struct UpdateBufs {
+  float* part;
+  int32_t* meta;
+  float* bpart;
+  int32_t* bmeta;
+  int64_t nunits, nblocks;
+};
+
+// Column slices per lane pass: VEC columns per lane (2 when D is even), NI
+// slices of 64 lanes per row (1, 2 or 4), and grid.z column blocks beyond.
+inline int runs_vec(int64_t D) { return D % 2 == 0 ? 2 : 1; }
+inline int runs_ni(int64_t D) {
+  const int64_t slices = (D + 64 * runs_vec(D) - 1) / (64 * runs_vec(D));
+  return slices <= 1 ? 1 : (slices <= 2 ? 2 : 4);
+}
+
 template <int DT, int VEC, int NI, bool INDEXED>
 int launch_runs_t(const void* x, const int32_t* perm, const int32_t* sids,
-                  float* sums, int32_t* counts, float* part, int32_t* meta,
-                  int64_t B, int64_t N, int64_t K, int64_t D, int64_t nunits,
-                  bool overwrite, const int32_t* ctrl, hipStream_t s) {
+                  float* sums, int32_t* counts, const UpdateBufs& w, int64_t B,
+                  int64_t N, int64_t K, int64_t D, bool overwrite,
+                  FinArgs<typename Elem<DT>::T> fin, const int32_t* ctrl,
+                  hipStream_t s) {
   using T = typename Elem<DT>::T;
   const int ur = choose_ur(B, N);
   const int64_t cols_per_block = 64 * VEC * NI;
-  dim3 grid((unsigned)((nunits + 3) / 4), (unsigned)B,
+  dim3 grid((unsigned)((w.nunits + 3) / 4), (unsigned)B,
             (unsigned)((D + cols_per_block - 1) / cols_per_block));
   hipLaunchKernelGGL((update_runs_kernel<DT, VEC, NI, INDEXED>), grid,
                      dim3(UT), 0, s, static_cast<const T*>(x), perm, sids,
-                     sums, counts, part, meta, (int)N, (int)K, (int)D,
-                     (int)nunits, ur, overwrite ? 1 : 0, ctrl);
+                     sums, counts, w.part, w.meta, (int)N, (int)K, (int)D,
+                     (int)w.nunits, ur, overwrite ? 1 : 0, fin, ctrl);
   return check_launch("update_runs");
 }
 
 template <int DT, bool INDEXED>
 int launch_runs_dt(const void* x, const int32_t* perm, const int32_t* sids,
-                   float* sums, int32_t* counts, float* part, int32_t* meta,
-                   int64_t B, int64_t N, int64_t K, int64_t D, int64_t nunits,
-                   bool overwrite, const int32_t* ctrl, hipStream_t s) {
-  const int vec = (D % 2 == 0) ? 2 : 1;
-  const int64_t slices = (D + 64 * vec - 1) / (64 * vec);
-#define FKC_RUNS(V, NI_)                                                    \
-  return launch_runs_t<DT, V, NI_, INDEXED>(x, perm, sids, sums, counts,   \
-                                            part, meta, B, N, K, D, nunits, \
-                                            overwrite, ctrl, s)
+                   float* sums, int32_t* counts, const UpdateBufs& w,
+                   int64_t B, int64_t N, int64_t K, int64_t D, bool overwrite,
+                   FinArgs<typename Elem<DT>::T> fin, const int32_t* ctrl,
+                   hipStream_t s) {
+#define FKC_RUNS(V, NI_)                                                      \
+  return launch_runs_t<DT, V, NI_, INDEXED>(x, perm, sids, sums, counts, w,  \
+                                            B, N, K, D, overwrite, fin, ctrl, \
+                                            s)
+  const int vec = runs_vec(D), ni = runs_ni(D);
   if (vec == 2) {
-    if (slices <= 1) FKC_RUNS(2, 1);
-    if (slices <= 2) FKC_RUNS(2, 2);
+    if (ni == 1) FKC_RUNS(2, 1);
+    if (ni == 2) FKC_RUNS(2, 2);
     FKC_RUNS(2, 4);
   }
-  if (slices <= 1) FKC_RUNS(1, 1);
-  if (slices <= 2) FKC_RUNS(1, 2);
+  if (ni == 1) FKC_RUNS(1, 1);
+  if (ni == 2) FKC_RUNS(1, 2);
   FKC_RUNS(1, 4);
 #undef FKC_RUNS
+}
+
+template <int DT>
+int launch_update_t(const void* x, const int32_t* perm,
+                    const int32_t* ids_sorted, float* sums, int32_t* counts,
+                    const UpdateBufs& w, int64_t B, int64_t N, int64_t K,
+                    int64_t D, bool overwrite, FinArgs<typename Elem<DT>::T> fin,
+                    const int32_t* ctrl, hipStream_t s) {
+  int rc = perm != nullptr
+               ? launch_runs_dt<DT, true>(x, perm, ids_sorted, sums, counts, w,
+                                          B, N, K, D, overwrite, fin, ctrl, s)
+               : launch_runs_dt<DT, false>(x, perm, ids_sorted, sums, counts,
+                                           w, B, N, K, D, overwrite, fin, ctrl,
+                                           s);
+  if (rc) return rc;
+  // With one block every run ends inside it and block partials are unused.
+  if (w.nblocks > 1) {
+    dim3 bgrid((unsigned)((w.nblocks + 3) / 4), (unsigned)B);
+    hipLaunchKernelGGL(update_blocks_kernel, bgrid, dim3(UT), 0, s, w.part,
+                       w.meta, w.bpart, w.bmeta, (int)D, (int)w.nunits,
+                       (int)w.nblocks, ctrl);
+    rc = check_launch("update_blocks");
+    if (rc) return rc;
+  }
+  dim3 grid((unsigned)((w.nunits + 3) / 4), (unsigned)B);
+  hipLaunchKernelGGL((update_merge_kernel<DT>), grid, dim3(UT), 0, s, w.part,
+                     w.meta, w.bpart, w.bmeta, sums, counts, (int)K, (int)D,
+                     (int)w.nunits, (int)w.nblocks, overwrite ? 1 : 0, fin,
+                     ctrl);
+  return check_launch("update_merge");
 }
 
 }  // namespace
@@ -534,7 +656,9 @@ int launch_update(const void* x, const int32_t* perm,
                   const int32_t* ids_sorted, float* sums, int32_t* counts,
                   int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
                   bool overwrite, void* ws, size_t ws_bytes,
-                  const int32_t* ctrl, hipStream_t s) {
+                  const int32_t* ctrl, hipStream_t s, const UpdateFinalize* fin,
+                  bool* fused) {
+  if (fused) *fused = false;
   if (B == 0) return FKC_OK;
   if (N == 0) {
     if (!overwrite) return FKC_OK;
@@ -550,57 +674,44 @@ int launch_update(const void* x, const int32_t* perm,
                 "centroid_update: workspace not %d-byte aligned",
                 kWorkspaceAlign);
   const int ur = choose_ur(B, N);
-  const int64_t nunits = (N + ur - 1) / ur;
+  UpdateBufs w;
+  w.nunits = (N + ur - 1) / ur;
+  w.nblocks = (w.nunits + UB - 1) / UB;
   Carve c(ws);
-  const int64_t nblocks = (nunits + UB - 1) / UB;
-  float* part = c.take<float>((size_t)B * nunits * 2 * D);
-  int32_t* meta = c.take<int32_t>((size_t)B * nunits * 4);
-  float* bpart = c.take<float>((size_t)B * nblocks * D);
-  int32_t* bmeta = c.take<int32_t>((size_t)B * nblocks * 2);
-  int rc = FKC_OK;
-  const bool idx = perm != nullptr;
+  w.part = c.take<float>((size_t)B * w.nunits * 2 * D);
+  w.meta = c.take<int32_t>((size_t)B * w.nunits * 4);
+  w.bpart = c.take<float>((size_t)B * w.nblocks * D);
+  w.bmeta = c.take<int32_t>((size_t)B * w.nblocks * 2);
+  // Finalize fuses when a whole row fits one wave's column slices and LDS
+  // row buffer (D <= 512; then grid.z == 1) and every label is valid.
+  const bool fuse = fin != nullptr && fin->cent != nullptr && overwrite &&
+                    D <= FIN_DMAX &&
+                    D <= (int64_t)64 * runs_vec(D) * runs_ni(D);
+  if (fused) *fused = fuse;
   switch (dtype) {
-    case FKC_F32:
-      rc = idx ? launch_runs_dt<FKC_F32, true>(x, perm, ids_sorted, sums, counts,
-                                               part, meta, B, N, K, D, nunits,
-                                               overwrite, ctrl, s)
-               : launch_runs_dt<FKC_F32, false>(x, perm, ids_sorted, sums,
-                                                counts, part, meta, B, N, K, D,
-                                                nunits, overwrite, ctrl, s);
-      break;
-    case FKC_F16:
-      rc = idx ? launch_runs_dt<FKC_F16, true>(x, perm, ids_sorted, sums, counts,
-                                               part, meta, B, N, K, D, nunits,
-                                               overwrite, ctrl, s)
-               : launch_runs_dt<FKC_F16, false>(x, perm, ids_sorted, sums,
-                                                counts, part, meta, B, N, K, D,
-                                                nunits, overwrite, ctrl, s);
-      break;
-    case FKC_BF16:
-      rc = idx ? launch_runs_dt<FKC_BF16, true>(x, perm, ids_sorted, sums,
-                                                counts, part, meta, B, N, K, D,
-                                                nunits, overwrite, ctrl, s)
-               : launch_runs_dt<FKC_BF16, false>(x, perm, ids_sorted, sums,
-                                                 counts, part, meta, B, N, K, D,
-                                                 nunits, overwrite, ctrl, s);
-      break;
+    case FKC_F32: {
+      FinArgs<float> f{fuse ? static_cast<float*>(fin->cent) : nullptr,
+                       fuse ? fin->c_sq : nullptr, fuse ? fin->shift : nullptr};
+      return launch_update_t<FKC_F32>(x, perm, ids_sorted, sums, counts, w, B,
+                                      N, K, D, overwrite, f, ctrl, s);
+    }
+    case FKC_F16: {
+      using T = typename Elem<FKC_F16>::T;
+      FinArgs<T> f{fuse ? static_cast<T*>(fin->cent) : nullptr,
+                   fuse ? fin->c_sq : nullptr, fuse ? fin->shift : nullptr};
+      return launch_update_t<FKC_F16>(x, perm, ids_sorted, sums, counts, w, B,
+                                      N, K, D, overwrite, f, ctrl, s);
+    }
+    case FKC_BF16: {
+      using T = typename Elem<FKC_BF16>::T;
+      FinArgs<T> f{fuse ? static_cast<T*>(fin->cent) : nullptr,
+                   fuse ? fin->c_sq : nullptr, fuse ? fin->shift : nullptr};
+      return launch_update_t<FKC_BF16>(x, perm, ids_sorted, sums, counts, w, B,
+                                       N, K, D, overwrite, f, ctrl, s);
+    }
     default:
       return fail(FKC_ERR_INVALID, "centroid_update: unknown dtype %d", dtype);
   }
-  if (rc) return rc;
-  // With one block every run ends inside it and block partials are unused.
-  if (nblocks > 1) {
-    dim3 bgrid((unsigned)((nblocks + 3) / 4), (unsigned)B);
-    hipLaunchKernelGGL(update_blocks_kernel, bgrid, dim3(UT), 0, s, part, meta,
-                       bpart, bmeta, (int)D, (int)nunits, (int)nblocks, ctrl);
-    rc = check_launch("update_blocks");
-    if (rc) return rc;
-  }
-  dim3 grid((unsigned)((nunits + 3) / 4), (unsigned)B);
-  hipLaunchKernelGGL(update_merge_kernel, grid, dim3(UT), 0, s, part, meta,
-                     bpart, bmeta, sums, counts, (int)K, (int)D, (int)nunits,
-                     (int)nblocks, overwrite ? 1 : 0, ctrl);
-  return check_launch("update_merge");
 }
 
 }  // namespace fkc

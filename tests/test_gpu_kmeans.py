@@ -217,6 +217,21 @@ def test_few_clusters_many_points(B, N, K, D, dtype):
     assert np.linalg.norm(gc - oc) / np.linalg.norm(oc) < 1e-2
 
 
+@pytest.mark.parametrize("D,dtype", [(512, "bf16"), (520, "f32"), (264, "f16"), (3, "f32")])
+def test_fused_loop_equals_per_op_path_across_widths(D, dtype):
+    """The loop finalizes inside the update for D <= 512 and with its own
+    kernel above; both must equal the per-op path (separate update and
+    finalize kernels, c_sq recomputed) bit for bit."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    rng = np.random.default_rng(D)
+    x = O.from_f32(rng.standard_normal((2, 3000, D)).astype(np.float32), dtype)
+    init = np.ascontiguousarray(x[:, :40])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a = batch_kmeans_Euclid(xt, 40, max_iters=3, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, 40, max_iters=3, init_centroids=it, verbose=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 def test_deterministic_loop():
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c3"]
