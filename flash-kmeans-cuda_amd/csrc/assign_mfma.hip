@@ -59,7 +59,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // for the lighter variants; FKC_EXACT_MAX_K, largest K that tracks the exact
 // index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
 // FKC_KC_DMA, centroid rows per direct stage (D <= 128); FKC_SCHED_GROUPS,
-// MFMA/VALU interleaving hints in the direct-stage loop.
+// LDS-read / MFMA / VALU ordering hints in the direct-stage loop.
 #ifndef FKC_AB
 #define FKC_AB 2
 #endif
@@ -74,12 +74,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #endif
 #ifndef FKC_SCHED_GROUPS
 #define FKC_SCHED_GROUPS 1
-#endif
-#ifndef FKC_SG_LEAD
-#define FKC_SG_LEAD 1
-#endif
-#ifndef FKC_SG_VALU
-#define FKC_SG_VALU 1
 #endif
 
 constexpr int KC = 64;  // centroid rows per register-staged LDS stage
@@ -206,78 +200,81 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
   };
 
   if constexpr (DMA) {
-    // Direct global->LDS stages.  A wave's load instruction writes 64 lanes
-    // x 16 bytes to consecutive LDS, so a stage row is stored unpadded as
-    // SEGS 16-byte slots, slot v holding feature segment v ^ swz(row): the
-    // sixteen rows a fragment read touches then fall on distinct banks.  The
-    // two stage buffers are separate arrays, so the compiler can tell that
-    // loads into one do not alias reads from the other and need not wait
-    // for them.  Each lane's source offset within a stage is fixed and the
-    // stage base is wave-uniform, so a stage's loads cost no vector ALU
-    // work.  With K >= KCD no row is clamped: the last stage starts at
-    // K - KCD instead, re-scoring rows an earlier stage saw (a re-seen row
-    // can never beat its own earlier score, so the first-maximum rule still
-    // holds, and every candidate row stays below K).  Only K < KCD clamps
-    // rows to K-1.  c_sq lands raw and each wave scales (and masks past K)
-    // its own share once its loads are in, before the barrier.
-    constexpr int KCD = DS2 <= 4 ? FKC_KC_DMA : 64;
+    // Direct global->LDS stages (buffer loads with the LDS bit).  A wave's
+    // load instruction writes 64 lanes x 16 bytes to consecutive LDS, so a
+    // stage row is stored unpadded as SEGS 16-byte slots, slot v holding
+    // feature segment v ^ swz(row): the sixteen rows a fragment read touches
+    // then fall on distinct banks.  The two stage buffers are separate
+    // arrays, so the compiler can tell that loads into one do not alias
+    // reads from the other.  Each stage is addressed through a buffer
+    // resource built from its wave-uniform base (scalar registers) plus a
+    // fixed 32-bit per-lane offset, so a stage's loads cost no vector ALU
+    // work and hold no 64-bit addresses in VGPRs.  Buffer (not global)
+    // loads also let the compiler wait for LDS reads by count while the
+    // next stage's loads are in flight; with global loads to LDS it waits
+    // for every outstanding LDS read at each use.  With K >= KCD no row is
+    // clamped: the last stage starts at K - KCD instead, re-scoring rows an
+    // earlier stage saw (a re-seen row can never beat its own earlier
+    // score, so the first-maximum rule still holds, and every candidate row
+    // stays below K).  Only K < KCD clamps rows to K-1.  c_sq lands raw and
+    // each wave scales (and masks past K) its own share once its loads are
+    // in, before the barrier.
+    constexpr int KCD0 = DS2 <= 4 ? FKC_KC_DMA : 64;
+    constexpr int KCD = (KCD0 * DP * 2) % (THREADS * 16) == 0 ? KCD0 : 64;
     constexpr int ROWB = DP * 2;
     constexpr int STAGE = KCD * ROWB;
     constexpr int LOADS = STAGE / (THREADS * 16);
     constexpr int QW = KCD / 4;  // c_sq entries loaded per wave
+    constexpr int RSRC_W3 = 0x00020000;  // buffer resource word 3 (gfx9)
     static_assert(STAGE % (THREADS * 16) == 0 && QW <= 64, "stage split");
     static_assert((ROWB & (ROWB - 1)) == 0, "power-of-two stage rows");
     __shared__ __attribute__((aligned(1024))) uint8_t s_c0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t s_c1[STAGE];
     __shared__ __attribute__((aligned(256))) float s_q0[KCD];
     __shared__ __attribute__((aligned(256))) float s_q1[KCD];
-    typedef __attribute__((address_space(1))) void gvoid;
     typedef __attribute__((address_space(3))) void lvoid;
 
     const int uwave = __builtin_amdgcn_readfirstlane(wave);  // scalar copy
-    // Source byte of load j within a stage: row * ROWB + permuted segment.
-    auto soff = [&](int j) {
-      const int pos = (uwave * LOADS + j) * 1024 + lane * 16;
-      const int r = pos / ROWB, v = (pos % ROWB) / 16;
-      return (uint32_t)(r * ROWB + (v ^ swz<SEGS>(r)) * 16);
-    };
-    uint32_t so[LOADS];
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) so[j] = soff(j);
-    const int qi = uwave * QW + lane;  // this lane's c_sq slot (lane < QW)
-    const int sw = swz<SEGS>(col);     // rows 16t + col share it
     const int nch = (K + KCD - 1) / KCD;
     const bool overlap = K >= KCD;     // wave-uniform
+    // Source byte of load j within a stage: row * ROWB + permuted segment
+    // (rows clamped to K-1 when K < KCD).
+    uint32_t so[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int pos = (uwave * LOADS + j) * 1024 + lane * 16;
+      const int r = pos / ROWB, v = (pos % ROWB) / 16;
+      so[j] = (uint32_t)((overlap ? r : min(r, K - 1)) * ROWB +
+                         (v ^ swz<SEGS>(r)) * 16);
+    }
+    const int qi = uwave * QW + lane;  // this lane's c_sq slot (lane < QW)
+    const uint32_t qo = (uint32_t)(overlap ? qi : min(qi, K - 1)) * 4;
+    const int sw = swz<SEGS>(col);     // rows 16t + col share it
     const char* cbase = reinterpret_cast<const char*>(cb);
-    auto kbase = [&](int chunk) {
-      return overlap ? min(chunk * KCD, K - KCD) : 0;
+    auto kbase = [&](int chunk) {      // first centroid row of a stage
+      return __builtin_amdgcn_readfirstlane(
+          overlap ? min(chunk * KCD, K - KCD) : 0);
     };
 
+    // (The offsets are passed through locals: with a captured variable as
+    // the offset argument this clang emits no host launch stub for the
+    // kernel.)
     auto issue = [&](int chunk, uint8_t* dc, float* dq) {
       const int kb = kbase(chunk);
-      const char* src = cbase + (size_t)kb * ROWB;
-      if (overlap) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(cbase + (size_t)kb * ROWB), 0, STAGE, RSRC_W3);
 #pragma unroll
-        for (int j = 0; j < LOADS; ++j)
-          __builtin_amdgcn_global_load_lds(
-              (gvoid*)(src + so[j]), (lvoid*)(dc + (uwave * LOADS + j) * 1024),
-              16, 0, 0);
-        if (lane < QW)
-          __builtin_amdgcn_global_load_lds((gvoid*)(qb + kb + qi),
-                                           (lvoid*)(dq + uwave * QW), 4, 0, 0);
-      } else {
-#pragma unroll
-        for (int j = 0; j < LOADS; ++j) {
-          const int r = (int)(so[j] / ROWB);
-          const uint32_t off =
-              (uint32_t)(min(r, K - 1) * ROWB) + so[j] % ROWB;
-          __builtin_amdgcn_global_load_lds(
-              (gvoid*)(src + off), (lvoid*)(dc + (uwave * LOADS + j) * 1024),
-              16, 0, 0);
-        }
-        if (lane < QW)
-          __builtin_amdgcn_global_load_lds((gvoid*)(qb + min(qi, K - 1)),
-                                           (lvoid*)(dq + uwave * QW), 4, 0, 0);
+      for (int j = 0; j < LOADS; ++j) {
+        const uint32_t off = so[j];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (lvoid*)(dc + (uwave * LOADS + j) * 1024), 16, off, 0, 0, 0);
+      }
+      if (lane < QW) {
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(qb + kb), 0, KCD * 4, RSRC_W3);
+        const uint32_t off = qo;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rq, (lvoid*)(dq + uwave * QW), 4, off, 0, 0, 0);
       }
     };
     // After this wave's loads have landed: scale its c_sq share in place.
@@ -299,13 +296,18 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       for (int s = 0; s < DS2; ++s)
         a[s] = *reinterpret_cast<const u32x4*>(arow + (((4 * s + g) ^ sw) * 16));
     };
-    // Software-pipelined over the stage's 16-centroid blocks: block t-1 is
-    // folded on the vector ALU while block t is on the matrix core.  For
-    // four point tiles the scheduling groups ask the compiler to interleave
-    // them (MFMA, VALU) rather than issue the whole stage's MFMAs first and
-    // its folds last, which keeps every accumulator alive at once and
-    // serialises the two units within a wave (measured: 0.86 -> 0.81 ms at
-    // N=524288, K=8192, D=128; with fewer tiles the groups cost time).
+    // Software-pipelined over the stage's 16-centroid blocks: the fragments
+    // of block t+1 are read from LDS while block t is on the matrix core,
+    // and block t-1 is folded on the vector ALU under block t's MFMAs.  For
+    // four point tiles the scheduling groups fix that order (LDS reads for
+    // the next block first, then MFMA / VALU alternating) rather than let
+    // the compiler issue the whole stage's MFMAs first and its folds last,
+    // which keeps every accumulator alive at once and serialises the two
+    // units within a wave, or read each fragment just before its MFMA,
+    // which exposes the LDS latency every 4 MFMAs (measured at N=524288,
+    // K=8192, D=128: 0.86 -> 0.81 ms for the MFMA/VALU groups, a further
+    // 0.79 -> 0.76 ms for the read-ahead; with fewer tiles the groups cost
+    // time).
     auto compute = [&](int chunk, const uint8_t* lc, const float* lq) {
       const int kb = kbase(chunk);
       constexpr int NTD = KCD / 16;
@@ -329,11 +331,16 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
         }
       } else {
         f32x4 prev[PT];
+        u32x4 an[DS2];  // fragments of the next block
+        f32x4 cn;
+        frag(lc, lq, 0, an, cn);
 #pragma unroll
         for (int t = 0; t < NTD; ++t) {
           u32x4 a[DS2];
-          f32x4 ci;
-          frag(lc, lq, t, a, ci);
+          f32x4 ci = cn;
+#pragma unroll
+          for (int s = 0; s < DS2; ++s) a[s] = an[s];
+          if (t + 1 < NTD) frag(lc, lq, t + 1, an, cn);
           f32x4 acc[PT];
 #pragma unroll
           for (int s = 0; s < DS2; ++s) {
@@ -343,14 +350,16 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
           }
           if (t > 0) fold(prev, kb + 16 * (t - 1));
           if constexpr (FKC_SCHED_GROUPS && PT >= 4) {
-            // FKC_SG_LEAD MFMAs first (distance from the previous block's
-            // last MFMA to the first fold op that reads it), then one
-            // MFMA per FKC_SG_VALU vector ops.
+            // Block 0 also takes block 1's reads (a stage's first two
+            // blocks are read back to back after the barrier).
+            if (t == 0 && NTD > 1)
+              __builtin_amdgcn_sched_group_barrier(0x100, 2 * (DS2 + 1), 0);
+            else if (t + 1 < NTD)
+              __builtin_amdgcn_sched_group_barrier(0x100, DS2 + 1, 0);
 #pragma unroll
             for (int i = 0; i < DS2 * PT; ++i) {
               __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-              if (i + 1 >= FKC_SG_LEAD)
-                __builtin_amdgcn_sched_group_barrier(0x002, FKC_SG_VALU, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
             }
           }
 #pragma unroll
@@ -360,6 +369,9 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       }
     };
 
+    // The wait for the next stage's loads stays at the end of the stage:
+    // the scheduling barrier keeps the compiler from hoisting it above the
+    // stage's matrix work.
     issue(0, s_c0, s_q0);
     __builtin_amdgcn_s_waitcnt(0);
     fixq(0, s_q0);
@@ -367,12 +379,14 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     for (int chunk = 0; chunk < nch; chunk += 2) {
       if (chunk + 1 < nch) issue(chunk + 1, s_c1, s_q1);
       compute(chunk, s_c0, s_q0);
+      __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(0);
       fixq(chunk + 1, s_q1);  // harmless on a stage that was not loaded
       __syncthreads();
       if (chunk + 1 >= nch) break;
       if (chunk + 2 < nch) issue(chunk + 2, s_c0, s_q0);
       compute(chunk + 1, s_c1, s_q1);
+      __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(0);
       fixq(chunk + 2, s_q0);
       __syncthreads();
