@@ -25,6 +25,8 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c5]
        python bench.py --report        per-config table (c1..c5): assign TFLOPS,
                                        ms/iter (steady state and one-iteration
                                        call), roofline fraction ideal/measured
+       python bench.py --gemm-peak     hipBLASLt GEMM TFLOP/s (practical
+                                       matrix-core ceiling on this part)
        python bench.py --traffic-probe / --lloyd-probe   workloads for
                                        rocprofv3 --pmc runs (see profiles/)
 """
@@ -133,6 +135,41 @@ def _lloyd_probe(cfg) -> int:
     return 0
 
 
+def _gemm_peak() -> int:
+    """Practical matrix-core ceiling on this part: torch.matmul (hipBLASLt)
+    on large square fp16 / bf16 GEMMs, plus the assign-shaped products
+    (inner dimension 128), median of 5 x 10 launches with HIP events on the
+    current stream.  One JSON line per shape."""
+    import statistics
+    import torch
+    shapes = [(8192, 8192, 8192), (16384, 16384, 8192), (8192, 8192, 16384),
+              (65536, 8192, 128), (524288, 1024, 128)]
+    for (m, n, k) in shapes:
+        for dt in (torch.float16, torch.bfloat16):
+            g = torch.Generator(device="cuda").manual_seed(0)
+            a = torch.randn(m, k, device="cuda", generator=g).to(dt)
+            b = torch.randn(k, n, device="cuda", generator=g).to(dt)
+            for _ in range(3):
+                c = a @ b
+            ts = []
+            for _ in range(5):
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(10):
+                    c = a @ b
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1) / 10)
+            ms = statistics.median(ts)
+            print(json.dumps({"M": m, "N": n, "K": k, "dtype": str(dt).replace("torch.", ""),
+                              "ms": round(ms, 4),
+                              "tflops": round(2.0 * m * n * k / ms / 1e9, 1)}), flush=True)
+            del a, b, c
+    return 0
+
+
 def _ideal_ms(cfg) -> tuple[float, float, float]:
     """(assign flops, bytes moved per iteration, ideal ms per iteration) from
     the algorithmic work: 2BNKD flops at the MFMA peak (VALU fp32 peak for
@@ -234,6 +271,9 @@ def main() -> int:
     ap.add_argument("--lloyd-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: the calibration copy, then 4 "
                          "one-iteration Lloyd calls")
+    ap.add_argument("--gemm-peak", action="store_true",
+                    help="practical matrix-core ceiling: hipBLASLt GEMM TFLOP/s "
+                         "(torch.matmul) on large fp16 / bf16 shapes")
     ap.add_argument("--report", nargs="?", const="c1,c2,c3,c4,c5", default=None,
                     help="per-configuration table (comma-separated config names)")
     args = ap.parse_args()
@@ -250,6 +290,8 @@ def main() -> int:
 
     if args.report:
         return _report(args.report.split(","))
+    if args.gemm_peak:
+        return _gemm_peak()
     cfg = synth.CONFIGS[args.config]
     if args.traffic_probe:
         return _traffic_probe(cfg)

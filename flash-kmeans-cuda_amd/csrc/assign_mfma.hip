@@ -44,6 +44,7 @@
 #include "device_util.hpp"
 #include "fkc_internal.hpp"
 
+#include <hip/hip_ext.h>
 #include <math.h>
 
 namespace fkc {
@@ -551,23 +552,33 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
   }
 }
 
+// ev0 / ev1 (both null or both set): events that the dispatch packet itself
+// stamps at the kernel's start and end (no marker packets in the stream).
 template <int DT, int DS2, int PT, bool PAD, bool EXACT>
 int launch_mfma_t(const void* x, const void* c, const float* c_sq,
                   int32_t* ids, int64_t B, int64_t N, int64_t K, int64_t D,
-                  const int32_t* ctrl, hipStream_t s) {
+                  const int32_t* ctrl, hipStream_t s, hipEvent_t ev0,
+                  hipEvent_t ev1) {
   constexpr int PTS_WG = 4 * PT * 16;
   dim3 grid((unsigned)((N + PTS_WG - 1) / PTS_WG), (unsigned)B);
-  hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
-                     dim3(THREADS),
-                     0, s, static_cast<const uint16_t*>(x),
-                     static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
-                     (int)K, (int)D, ctrl);
+  if (ev0 != nullptr)
+    hipExtLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
+                          dim3(THREADS), 0, s, ev0, ev1, 0,
+                          static_cast<const uint16_t*>(x),
+                          static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
+                          (int)K, (int)D, ctrl);
+  else
+    hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
+                       dim3(THREADS), 0, s, static_cast<const uint16_t*>(x),
+                       static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
+                       (int)K, (int)D, ctrl);
   return check_launch("assign_mfma");
 }
 
 using MfmaLauncher = int (*)(const void*, const void*, const float*, int32_t*,
                              int64_t, int64_t, int64_t, int64_t,
-                             const int32_t*, hipStream_t);
+                             const int32_t*, hipStream_t, hipEvent_t,
+                             hipEvent_t);
 
 template <int DT, int DS2, int PT>
 constexpr MfmaLauncher entry(bool pad, bool exact) {
@@ -643,7 +654,7 @@ static int choose_pt(int ds2, int64_t B, int64_t N) {
 int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                        int32_t* ids, int64_t B, int64_t N, int64_t K,
                        int64_t D, int dtype, const int32_t* ctrl,
-                       hipStream_t s) {
+                       hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   const int ds2 = (int)((D + 31) / 32);
   const int pt = choose_pt(ds2, B, N);
   const bool pad = D != 32 * ds2;
@@ -656,7 +667,7 @@ int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
   if (!fn)
     return fail(FKC_ERR_UNSUPPORTED, "assign: no MFMA variant for D=%lld",
                 (long long)D);
-  return fn(x, c, c_sq, ids, B, N, K, D, ctrl, s);
+  return fn(x, c, c_sq, ids, B, N, K, D, ctrl, s, ev0, ev1);
 }
 
 }  // namespace fkc

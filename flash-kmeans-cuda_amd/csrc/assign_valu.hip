@@ -26,7 +26,7 @@ namespace fkc {
 int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                        int32_t* ids, int64_t B, int64_t N, int64_t K,
                        int64_t D, int dtype, const int32_t* ctrl,
-                       hipStream_t s);
+                       hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
 
 namespace {
 
@@ -198,19 +198,29 @@ int launch_rowsq_t(const void* src, float* out, int64_t rows, int64_t D,
 int launch_assign(const void* x, const void* c, const float* x_sq,
                   const float* c_sq, int32_t* ids, int64_t B, int64_t N,
                   int64_t K, int64_t D, int dtype, const int32_t* ctrl,
-                  hipStream_t s) {
+                  hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (B == 0 || N == 0) return FKC_OK;
   if (assign_uses_mfma(dtype, D))
-    return launch_assign_mfma(x, c, c_sq, ids, B, N, K, D, dtype, ctrl, s);
+    return launch_assign_mfma(x, c, c_sq, ids, B, N, K, D, dtype, ctrl, s,
+                              ev0, ev1);
+  // The VALU route marks its span with event records on the stream.
+  if (ev0 != nullptr) (void)hipEventRecord(ev0, s);
+  int rc = FKC_OK;
   switch (dtype) {
     case FKC_F32:
-      return launch_valu_t<FKC_F32>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+      rc = launch_valu_t<FKC_F32>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+      break;
     case FKC_F16:
-      return launch_valu_t<FKC_F16>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+      rc = launch_valu_t<FKC_F16>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+      break;
     case FKC_BF16:
-      return launch_valu_t<FKC_BF16>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+      rc = launch_valu_t<FKC_BF16>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
+      break;
+    default:
+      return fail(FKC_ERR_INVALID, "assign: unknown dtype %d", dtype);
   }
-  return fail(FKC_ERR_INVALID, "assign: unknown dtype %d", dtype);
+  if (ev1 != nullptr) (void)hipEventRecord(ev1, s);
+  return rc;
 }
 
 int launch_row_sqnorm(const void* src, float* out, int64_t rows, int64_t D,

@@ -49,6 +49,13 @@ int ntiles_override() {
   return (v == 1 || v == 2 || v == 4) ? v : 0;
 }
 
+int sort_tile_override() {
+  const char* s = std::getenv("FKC_SORT_TILE");
+  if (!s) return 0;
+  const int v = std::atoi(s);
+  return (v == 256 || v == 512 || v == 1024 || v == 2048 || v == 4096) ? v : 0;
+}
+
 // ------------------------------------------------------------- profiling
 namespace {
 struct Profile {
@@ -306,27 +313,26 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
   const int32_t* ctrl = check ? L.ctrl : nullptr;
   int rc = launch_fill_i32(L.ctrl, 0, 4, s);
   if (!rc && check) rc = launch_fill_f32(L.shift, 0.f, max_iters, s);
+  if (!rc) rc = label_sort_reset(L.sort_ws, B, N, K, s);
   if (!rc && L.x_sq) rc = launch_row_sqnorm(x, L.x_sq, B * N, D, dtype, nullptr, s);
   if (!rc) rc = launch_row_sqnorm(centroids, L.c_sq, B * K, D, dtype, nullptr, s);
   if (rc) return rc;
 
   for (int it = 0; it < max_iters; ++it) {
+    // Profiling: the assign's dispatch stamps the two events (no marker
+    // packets between the iteration's kernels).
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (g_prof.enabled) {
-      (void)hipEventCreate(&e0);
-      (void)hipEventCreate(&e1);
-      (void)hipEventRecord(e0, s);
-    }
-    rc = launch_assign(x, centroids, L.x_sq, L.c_sq, cluster_ids, B, N, K, D,
-                       dtype, ctrl, s);
-    if (g_prof.enabled) {
-      (void)hipEventRecord(e1, s);
+      if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+        return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: profiling event creation failed");
       g_prof.starts.push_back(e0);
       g_prof.stops.push_back(e1);
     }
+    rc = launch_assign(x, centroids, L.x_sq, L.c_sq, cluster_ids, B, N, K, D,
+                       dtype, ctrl, s, e0, e1);
     if (!rc)
       rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
-                             L.sort_ws, L.sort_ws_bytes, ctrl, s);
+                             L.sort_ws, L.sort_ws_bytes, ctrl, s, it & 1);
     // The update finalizes the centroids itself when D <= 512 (no sums /
     // counts round trip); otherwise finalize runs as its own kernel.
     const UpdateFinalize fin{centroids, L.c_sq, check ? L.shift + it : nullptr};

@@ -40,10 +40,13 @@ struct Carve {
 // ---------------------------------------------------------------- assign
 // Routing predicate: the MFMA kernel serves fp16/bf16, D % 8 == 0, D <= 512.
 bool assign_uses_mfma(int dtype, int64_t D);
+// ev0 / ev1 (optional, both or neither): timing events of the launch; on
+// the MFMA route the dispatch packet stamps them (no extra stream packets).
 int launch_assign(const void* x, const void* c, const float* x_sq,
                   const float* c_sq, int32_t* ids, int64_t B, int64_t N,
                   int64_t K, int64_t D, int dtype, const int32_t* ctrl,
-                  hipStream_t s);
+                  hipStream_t s, hipEvent_t ev0 = nullptr,
+                  hipEvent_t ev1 = nullptr);
 int launch_row_sqnorm(const void* src, float* out, int64_t rows, int64_t D,
                       int dtype, const int32_t* ctrl, hipStream_t s);
 
@@ -59,10 +62,16 @@ struct SortPlan {
 // the sentinel bin (K = 256 then sorts in one 8-bit pass).
 SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid);
 size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K);
+// phase < 0: standalone call (clears its digit counts first).  phase 0 / 1:
+// the caller alternates phases over consecutive calls on one workspace and
+// cleared it once with label_sort_reset before the first (phase 0) call.
 int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
                       int64_t B, int64_t N, int64_t K, bool labels_valid,
                       void* ws, size_t ws_bytes, const int32_t* ctrl,
-                      hipStream_t s);
+                      hipStream_t s, int phase = -1);
+int label_sort_reset(void* ws, int64_t B, int64_t N, int64_t K, hipStream_t s);
+// FKC_SORT_TILE=256|512|1024|2048|4096: keys per sort tile; 0 = auto.
+int sort_tile_override();
 
 // ---------------------------------------------------------------- update
 size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D);

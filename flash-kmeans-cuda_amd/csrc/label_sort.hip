@@ -7,20 +7,36 @@
 // bits = ceil(log2(K+1)) so the sentinel has a bin, or ceil(log2(K)) when the
 // caller vouches that every label is valid (labels straight from the assign
 // kernel), split into passes of at most 8 bits.
-// Each pass is reduce-then-scan, with no inter-workgroup waiting:
-//   sort_hist    : per tile of 4096 keys (1024 for small N), a digit
-//                  histogram in LDS, written digit-major to
-//                  hist[b][digit][tile];
-//   sort_scan    : exclusive scan of hist[b] (digit-major, so the scan gives
-//                  every (digit, tile) its global output offset);
-//   sort_scatter : each wave ranks its share of the tile (8 waves x 512
-//                  keys, or 4 waves x 256 keys for 1024-key tiles) stably,
-//                  64 keys at a time: a ballot per digit bit yields, for every lane, the
-//                  mask of lanes holding the same digit ("multi-split"); its
-//                  rank is the per-wave digit counter plus the matching lanes
-//                  below it.  Keys are placed in LDS in tile-sorted order,
-//                  then each digit's run is copied to its global slot, so the
-//                  writes are runs of consecutive addresses.
+//
+// One read of the keys counts the digits of every pass, then each pass is a
+// single kernel that places its tile's keys using a chained scan with
+// decoupled look-back (Merrill & Garland, "Single-pass Parallel Prefix Scan
+// with Decoupled Look-back", 2016; the radix-sort form is Adinets & Merrill,
+// "Onesweep", 2022):
+//   sort_upsweep  : digit histograms of all passes in LDS, added into the
+//                   global per-pass digit counts; also clears the tile
+//                   status words and tile counters the passes will use.
+//   sort_onesweep : a workgroup takes the next tile index from a counter (so
+//                   every tile it waits for is already running), ranks its
+//                   keys stably by digit (per 64-key chunk, one ballot per
+//                   digit bit gives every lane the mask of lanes holding its
+//                   digit, "multi-split"), publishes its per-digit counts,
+//                   then walks back over earlier tiles' status words, adding
+//                   their counts until it meets an inclusive prefix, and
+//                   publishes its own inclusive prefix.  Keys are placed in
+//                   LDS in tile-sorted order and each digit's run is copied
+//                   to its global slot, so writes are runs of consecutive
+//                   addresses.
+// A status word is 64 bits: flag in bits 63..62 (published count, or
+// inclusive prefix), count in the rest, read and written with relaxed
+// agent-scope atomics, so a reader sees flag and count together and no fence
+// is needed.  Each wait is bounded: past the spin limit the tile records an
+// error in the workspace and proceeds, so every workgroup always exits.
+//
+// The global digit counts accumulate into one of two buffers (the call's
+// phase); the upsweep clears the other, so a caller that alternates phases
+// (the Lloyd loop) clears once per loop, and a standalone call clears its
+// phase-0 buffer first.
 // The carried payload is the original index; the last pass writes the
 // user's sorted_ids / perm.
 #include "device_util.hpp"
@@ -29,136 +45,171 @@
 namespace fkc {
 namespace {
 
-constexpr int HT = 256;           // threads of the histogram kernel
+constexpr int MAXP = 4;           // passes at most (31-bit keys, 8-bit digits)
+constexpr int UPT = 512;          // threads of the upsweep kernel
+constexpr uint64_t ST_AGG = 1ull << 62;  // the tile's own digit count
+constexpr uint64_t ST_INC = 2ull << 62;  // inclusive prefix over tiles 0..t
+constexpr uint64_t ST_VAL = (1ull << 62) - 1;
+constexpr int SPIN_LIMIT = 1 << 18;  // empty polls per thread and pass (< 1 s)
 
-// Keys per tile (one workgroup of each kernel): 4096, or 1024 for small N so
-// that the grid still has some width.
+struct PassDesc {
+  int passes;
+  int bits[MAXP];
+  int shift[MAXP];
+};
+
+// Threads of the onesweep kernel per tile size.
 template <int TILE_>
 struct Geom {
   static constexpr int TILE = TILE_;
-  static constexpr int ST = TILE_ >= 4096 ? 512 : 256;  // scatter threads
-  static constexpr int SW = ST / 64;                    // scatter waves
+  static constexpr int ST = TILE_ >= 4096 ? 512 : 256;
+  static constexpr int SW = ST / 64;
   static constexpr int PER_WAVE = TILE / SW;
   static constexpr int CHUNKS = PER_WAVE / 64;
-  static_assert(ST >= 256 && CHUNKS >= 1, "scatter geometry");
+  static_assert(CHUNKS >= 1 && PER_WAVE % 64 == 0, "onesweep geometry");
 };
 
 __device__ inline uint32_t sort_key(int32_t id, int K) {
   return (uint32_t)id < (uint32_t)K ? (uint32_t)id : (uint32_t)K;
 }
 
-// Per-batch stride of the digit table: room for 256 digits x ntiles,
-// rounded to whole int4s so every batch row starts 16-byte aligned.
-inline int64_t table_stride(int64_t ntiles) { return (256 * ntiles + 3) / 4 * 4; }
+// Workspace layout, shared by the size query and the launcher.
+struct SortBufs {
+  int32_t* err;      // [1] look-back spin limit reached (never in a good run)
+  int32_t* gcnt;     // [2 phases][B][MAXP][256] global digit counts; err and
+                     // phase 0 are contiguous (one fill clears both)
+  int32_t* tctr;     // [B][MAXP] tile counters
+  uint64_t* status;  // [B][P][ntiles][256] tile status words
+  int32_t* tk[2];    // ping buffers: keys
+  int32_t* tv[2];    //               payload
+  int64_t gphase;    // int32 entries per phase of gcnt
+  int64_t slen;      // status words per batch row
+};
 
-template <int TILE>
-__global__ void __launch_bounds__(HT)
-sort_hist_kernel(const int32_t* __restrict__ keys, int32_t* __restrict__ hist,
-                 int N, int K, int shift, int bits, int ntiles, int64_t hstride,
-                 const int32_t* __restrict__ ctrl) {
+SortBufs carve_sort(void* ws, int64_t B, int64_t N, int64_t K, size_t* used) {
+  const SortPlan p = sort_plan(B, N, K, false);  // the larger of the two plans
+  Carve c(ws);
+  SortBufs s{};
+  s.gphase = B * MAXP * 256;
+  s.err = c.take<int32_t>((size_t)64 + 2 * s.gphase);
+  s.gcnt = s.err ? s.err + 64 : nullptr;
+  s.tctr = c.take<int32_t>((size_t)B * MAXP);
+  s.slen = (int64_t)p.passes * p.ntiles * 256;
+  s.status = c.take<uint64_t>((size_t)B * s.slen);
+  const int tmp = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
+  for (int i = 0; i < tmp; ++i) {
+    s.tk[i] = c.take<int32_t>((size_t)B * N);
+    s.tv[i] = c.take<int32_t>((size_t)B * N);
+  }
+  if (used) *used = c.used;
+  return s;
+}
+
+// Digit counts of every pass over this workgroup's keys, added into
+// gcnt_cur; the workgroup also clears its share of the row's status words,
+// and workgroup 0 the row's tile counters and the other phase's counts.
+__global__ void __launch_bounds__(UPT)
+sort_upsweep_kernel(const int32_t* __restrict__ keys, int N, int K,
+                    PassDesc pd, int per_wg, int32_t* __restrict__ gcnt_cur,
+                    int32_t* __restrict__ gcnt_next,
+                    uint64_t* __restrict__ status, int64_t slen,
+                    int32_t* __restrict__ tctr,
+                    const int32_t* __restrict__ ctrl) {
   if (loop_done(ctrl)) return;
-  __shared__ int h[256];
-  const int nb = 1 << bits;
+  __shared__ int h[MAXP][256];
   const int tid = threadIdx.x;
-  const int tile = blockIdx.x, b = blockIdx.y;
-  if (tid < nb) h[tid] = 0;
+  const int w = blockIdx.x, b = blockIdx.y, U = gridDim.x;
+  for (int i = tid; i < MAXP * 256; i += UPT) (&h[0][0])[i] = 0;
+  {
+    // slen is a multiple of 256, so every share is whole 16-byte pairs.
+    const int64_t per = ((slen + U - 1) / U + 1) / 2 * 2;
+    const int64_t lo = min((int64_t)w * per, slen);
+    const int64_t hi = min(lo + per, slen);
+    uint64_t* sb = status + (size_t)b * slen;
+    for (int64_t i = lo + 2 * tid; i < hi; i += 2 * UPT)
+      *reinterpret_cast<ulonglong2*>(sb + i) = ulonglong2{0ull, 0ull};
+  }
+  if (w == 0) {
+    for (int i = tid; i < MAXP * 256; i += UPT)
+      gcnt_next[(size_t)b * MAXP * 256 + i] = 0;
+    if (tid < MAXP) tctr[(size_t)b * MAXP + tid] = 0;
+  }
   __syncthreads();
   const int32_t* kb = keys + (size_t)b * N;
-  const int base = tile * TILE;
-  const uint32_t dmask = (uint32_t)(nb - 1);
-  for (int i = tid; i < TILE; i += HT) {
-    const int n = base + i;
-    if (n < N) atomicAdd(&h[(sort_key(kb[n], K) >> shift) & dmask], 1);
+  const int lo = w * per_wg, hi = min(lo + per_wg, N);
+  for (int n = lo + tid; n < hi; n += UPT) {
+    const uint32_t key = sort_key(kb[n], K);
+    for (int p = 0; p < pd.passes; ++p)
+      atomicAdd(&h[p][(key >> pd.shift[p]) & ((1u << pd.bits[p]) - 1u)], 1);
   }
   __syncthreads();
-  if (tid < nb) hist[(size_t)b * hstride + (size_t)tid * ntiles + tile] = h[tid];
+  for (int i = tid; i < pd.passes * 256; i += UPT) {
+    const int v = (&h[0][0])[i];
+    if (v) atomicAdd(&gcnt_cur[(size_t)b * MAXP * 256 + i], v);
+  }
 }
 
-// In-place exclusive scan of one batch row of the digit table (len = bins x
-// ntiles entries, digit-major).  One 1024-thread workgroup per batch row;
-// each thread owns a contiguous, 4-aligned segment read with 16-byte loads.
-__global__ void __launch_bounds__(1024)
-sort_scan_kernel(int32_t* __restrict__ hist, int64_t len, int64_t hstride,
-                 const int32_t* __restrict__ ctrl) {
-  if (loop_done(ctrl)) return;
-  __shared__ int wsum[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int32_t* hb = hist + (size_t)blockIdx.x * hstride;
-  const int64_t per = ((len + 1023) / 1024 + 3) / 4 * 4;
-  const int64_t lo = min((int64_t)tid * per, len);
-  const int64_t hi = min(lo + per, len);
-  int local = 0;
-  int64_t i = lo;
-  for (; i + 4 <= hi; i += 4) {
-    const int4 v = *reinterpret_cast<const int4*>(hb + i);
-    local += v.x + v.y + v.z + v.w;
-  }
-  for (; i < hi; ++i) local += hb[i];
-  int incl = local;
+// Exclusive scan over the 256 digits of two values at once (digit = tid for
+// threads 0..255; wtot holds 2 x 4 wave totals).  Every thread of the
+// workgroup calls it (it contains a barrier); waves past the fourth pass
+// zeros and their results are unused.  Returns the exclusive prefixes.
+__device__ inline int2 scan256x2(int a, int c, int* wtot, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  int ia = a, ic = c;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int v = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += v;
-  }
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  if (tid < 64) {
-    int v = tid < 16 ? wsum[tid] : 0;
-    int inc = v;
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-      const int u = __shfl_up(inc, off, 64);
-      if (tid >= off) inc += u;
+    const int ua = __shfl_up(ia, off, 64);
+    const int uc = __shfl_up(ic, off, 64);
+    if (lane >= off) {
+      ia += ua;
+      ic += uc;
     }
-    if (tid < 16) wsum[tid] = inc - v;
+  }
+  if (lane == 63 && wave < 4) {
+    wtot[wave] = ia;
+    wtot[4 + wave] = ic;
   }
   __syncthreads();
-  int run = wsum[wave] + incl - local;  // exclusive prefix of this thread
-  i = lo;
-  for (; i + 4 <= hi; i += 4) {
-    int4 v = *reinterpret_cast<const int4*>(hb + i);
-    int4 o;
-    o.x = run; run += v.x;
-    o.y = run; run += v.y;
-    o.z = run; run += v.z;
-    o.w = run; run += v.w;
-    *reinterpret_cast<int4*>(hb + i) = o;
+  int ba = 0, bc = 0;
+  for (int w = 0; w < min(wave, 4); ++w) {
+    ba += wtot[w];
+    bc += wtot[4 + w];
   }
-  for (; i < hi; ++i) {
-    const int v = hb[i];
-    hb[i] = run;
-    run += v;
-  }
+  return int2{ba + ia - a, bc + ic - c};
 }
 
-// Stable rank of every key of one tile by its digit, then a coalesced
-// write-out: keys are first placed in LDS in tile-sorted order, then each
-// digit's contiguous run is copied to its global slot.
 template <int TILE, int ST = Geom<TILE>::ST>
 __global__ void __launch_bounds__(ST)
-sort_scatter_kernel(const int32_t* __restrict__ keys_in,
-                    const int32_t* __restrict__ vals_in,
-                    int32_t* __restrict__ keys_out,
-                    int32_t* __restrict__ vals_out,
-                    const int32_t* __restrict__ offs, int N, int K, int shift,
-                    int bits, int ntiles, int64_t hstride,
-                    const int32_t* __restrict__ ctrl) {
+sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
+                     const int32_t* __restrict__ vals_in,
+                     int32_t* __restrict__ keys_out,
+                     int32_t* __restrict__ vals_out,
+                     const int32_t* __restrict__ gcnt,  // this pass, row stride MAXP*256
+                     uint64_t* __restrict__ status,     // this pass, row stride slen
+                     int64_t slen, int32_t* __restrict__ tctr,  // this pass, row stride MAXP
+                     int32_t* __restrict__ err, int N, int K, int shift,
+                     int bits, const int32_t* __restrict__ ctrl) {
   constexpr int SW = Geom<TILE>::SW;
   constexpr int PER_WAVE = Geom<TILE>::PER_WAVE;
   constexpr int CHUNKS = Geom<TILE>::CHUNKS;
   if (loop_done(ctrl)) return;
   __shared__ int cnt[SW][256];
-  __shared__ int dstart[256];
   __shared__ int gbase[256];
-  __shared__ int wtot[4];
+  __shared__ int dstart[256];
+  __shared__ int wtot[8];
+  __shared__ int s_tile;
   __shared__ int32_t skey[TILE];
   __shared__ int32_t sval[TILE];
   const int nb = 1 << bits;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tile = blockIdx.x, b = blockIdx.y;
+  const int b = blockIdx.y;
+  // The pass's global digit count does not depend on the tile: its load is
+  // in flight together with the tile-counter atomic.
+  const int gc = tid < nb ? gcnt[(size_t)b * MAXP * 256 + tid] : 0;
   for (int i = tid; i < SW * 256; i += ST) (&cnt[0][0])[i] = 0;
-  if (tid < nb) gbase[tid] = offs[(size_t)b * hstride + (size_t)tid * ntiles + tile];
+  if (tid == 0) s_tile = atomicAdd(&tctr[(size_t)b * MAXP], 1);
   __syncthreads();
+  const int tile = s_tile;
 
   const int32_t* kb = keys_in + (size_t)b * N;
   const int32_t* vb = vals_in ? vals_in + (size_t)b * N : nullptr;
@@ -172,9 +223,13 @@ sort_scatter_kernel(const int32_t* __restrict__ keys_in,
   for (int c = 0; c < CHUNKS; ++c) {
     const int n = base + c * 64 + lane;
     const bool valid = n < N;
-    const int32_t key = valid ? kb[n] : 0;
-    const int32_t val = valid ? (vb ? vb[n] : n) : 0;
-    const uint32_t d = (sort_key(key, K) >> shift) & dmask;
+    kk[c] = valid ? kb[n] : 0;
+    vv[c] = valid ? (vb ? vb[n] : n) : 0;
+  }
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const bool valid = base + c * 64 + lane < N;
+    const uint32_t d = (sort_key(kk[c], K) >> shift) & dmask;
     uint64_t match = __builtin_amdgcn_ballot_w64(valid);
     for (int bit = 0; bit < bits; ++bit) {
       const bool on = (d >> bit) & 1u;
@@ -184,13 +239,13 @@ sort_scatter_kernel(const int32_t* __restrict__ keys_in,
     const uint32_t below = lanes_below(match);
     const int old = cnt[wave][d];
     if (valid && below == 0) cnt[wave][d] = old + __popcll(match);
-    kk[c] = key;
-    vv[c] = val;
     rank[c] = valid ? old + (int)below : -1;
     dig[c] = (int)d;
   }
   __syncthreads();
-  // per digit: offsets of each wave inside the digit, and the digit total
+
+  // Per digit: the waves' offsets inside the digit and the tile's count,
+  // published at once so later tiles can move on.
   int total = 0;
   if (tid < 256) {
     if (tid < nb) {
@@ -199,22 +254,40 @@ sort_scatter_kernel(const int32_t* __restrict__ keys_in,
         cnt[w][tid] = total;
         total += v;
       }
+      __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
+                         (tile == 0 ? ST_INC : ST_AGG) | (uint64_t)total,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // exclusive scan of digit totals over the 256 digits (waves 0..3)
-    int incl = total;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int u = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += u;
-    }
-    if (lane == 63) wtot[wave] = incl;
-    dstart[tid] = incl - total;  // within-wave exclusive prefix for now
   }
-  __syncthreads();
-  if (tid < 256) {
-    int add = 0;
-    for (int w = 0; w < wave; ++w) add += wtot[w];
-    dstart[tid] += add;
+  // Tile-local and global exclusive digit prefixes.
+  const int2 pre = scan256x2(total, gc, wtot, tid);
+  if (tid < nb) {
+    int64_t excl = 0;
+    if (tile > 0) {
+      const uint64_t* col = status + (size_t)b * slen + tid;
+      int spins = 0;  // one budget for the whole walk
+      for (int t = tile - 1;; --t) {
+        uint64_t v = 0;
+        for (;; ++spins) {
+          v = __hip_atomic_load(col + (size_t)t * 256, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+          if (v & (ST_AGG | ST_INC)) break;
+          if (spins >= SPIN_LIMIT) {
+            atomicOr(err, 1);
+            v = ST_INC;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        excl += (int64_t)(v & ST_VAL);
+        if ((v & ST_INC) || t == 0) break;
+      }
+      __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
+                         ST_INC | (uint64_t)(excl + total), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    dstart[tid] = pre.x;
+    gbase[tid] = pre.y + (int)excl - pre.x;
   }
   __syncthreads();
 #pragma unroll
@@ -231,10 +304,21 @@ sort_scatter_kernel(const int32_t* __restrict__ keys_in,
   for (int i = tid; i < tn; i += ST) {
     const int32_t key = skey[i];
     const int d = (int)((sort_key(key, K) >> shift) & dmask);
-    const int pos = gbase[d] + (i - dstart[d]);
+    const int pos = gbase[d] + i;
     ko[pos] = key;
     vo[pos] = sval[i];
   }
+}
+
+template <int TILE>
+void launch_onesweep(dim3 grid, hipStream_t s, const int32_t* kin,
+                     const int32_t* vin, int32_t* kout, int32_t* vout,
+                     const int32_t* gcnt, uint64_t* status, int64_t slen,
+                     int32_t* tctr, int32_t* err, int N, int K, int shift,
+                     int bits, const int32_t* ctrl) {
+  hipLaunchKernelGGL((sort_onesweep_kernel<TILE>), grid, dim3(Geom<TILE>::ST),
+                     0, s, kin, vin, kout, vout, gcnt, status, slen, tctr, err,
+                     N, K, shift, bits, ctrl);
 }
 
 }  // namespace
@@ -253,30 +337,28 @@ SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
     p.shift[i] = shift;
     shift += w;
   }
-  // 1024-key tiles widen the grid for small N; past 128 tiles per batch row
-  // the single-workgroup scan of the (256 x tiles) table costs more than the
-  // extra width saves (measured: N = 131072 gains, N = 524288 loses).
-  p.tile = N <= 131072 ? 1024 : 4096;
+  // 4096-key tiles: a pass costs a few dependent memory round trips per
+  // tile plus about 20 ns of look-back chain per tile, so fewer, larger
+  // tiles win even when they leave CUs idle (measured at N = 524288,
+  // K = 8192: 52 / 32 / 21 / 16 / 13.5 us per pass for 256 .. 4096-key
+  // tiles).  FKC_SORT_TILE overrides.
+  int tile = 4096;
+  if (const int o = sort_tile_override()) tile = o;
+  p.tile = tile;
   p.ntiles = (N + p.tile - 1) / p.tile;
   return p;
 }
 
 size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K) {
-  const SortPlan p = sort_plan(B, N, K, false);  // the larger of the two plans
-  Carve c(nullptr);
-  c.take<int32_t>((size_t)B * table_stride(p.ntiles));  // digit table
-  const int tmp = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
-  for (int i = 0; i < tmp; ++i) {
-    c.take<int32_t>((size_t)B * N);  // keys
-    c.take<int32_t>((size_t)B * N);  // payload
-  }
-  return c.used;
+  size_t used = 0;
+  carve_sort(nullptr, B, N, K, &used);
+  return used;
 }
 
 int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
                       int64_t B, int64_t N, int64_t K, bool labels_valid,
                       void* ws, size_t ws_bytes, const int32_t* ctrl,
-                      hipStream_t s) {
+                      hipStream_t s, int phase) {
   if (B == 0 || N == 0) return FKC_OK;
   const size_t need = sort_workspace_bytes(B, N, K);
   if (ws_bytes < need || (need > 0 && ws == nullptr))
@@ -286,56 +368,80 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
     return fail(FKC_ERR_WORKSPACE, "label_sort: workspace not %d-byte aligned",
                 kWorkspaceAlign);
   const SortPlan p = sort_plan(B, N, K, labels_valid);
-  Carve c(ws);
-  const int64_t hstride = table_stride(p.ntiles);
-  int32_t* hist = c.take<int32_t>((size_t)B * hstride);
-  int32_t* tk[2] = {nullptr, nullptr};
-  int32_t* tv[2] = {nullptr, nullptr};
-  const int tmp = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
-  for (int i = 0; i < tmp; ++i) {
-    tk[i] = c.take<int32_t>((size_t)B * N);
-    tv[i] = c.take<int32_t>((size_t)B * N);
-  }
   if (p.passes == 0) {  // K == 1 with valid labels: already sorted
     int rc = launch_fill_i32(sorted_ids, 0, B * N, s);
     return rc ? rc : launch_iota_i32(perm, B, N, s);
   }
+  SortBufs w = carve_sort(ws, B, N, K, nullptr);
+  if (phase < 0) {
+    int rc = launch_fill_i32(w.err, 0, 64 + w.gphase, s);
+    if (rc) return rc;
+    phase = 0;
+  }
+  int32_t* gcur = w.gcnt + (size_t)(phase & 1) * w.gphase;
+  int32_t* gnext = w.gcnt + (size_t)((phase & 1) ^ 1) * w.gphase;
+  PassDesc pd{};
+  pd.passes = p.passes;
+  for (int i = 0; i < p.passes; ++i) {
+    pd.bits[i] = p.bits[i];
+    pd.shift[i] = p.shift[i];
+  }
+  // Upsweep: about 128 workgroups per batch row, 1024..8192 keys each.
+  int per_wg = 1024;
+  while (per_wg < 8192 && (N + per_wg - 1) / per_wg > 128) per_wg <<= 1;
+  const int64_t slen = (int64_t)p.passes * p.ntiles * 256;
+  dim3 ugrid((unsigned)((N + per_wg - 1) / per_wg), (unsigned)B);
+  hipLaunchKernelGGL(sort_upsweep_kernel, ugrid, dim3(UPT), 0, s, ids, (int)N,
+                     (int)K, pd, per_wg, gcur, gnext, w.status, slen, w.tctr,
+                     ctrl);
+  int rc = check_launch("sort_upsweep");
+  if (rc) return rc;
+
   const int32_t* kin = ids;
   const int32_t* vin = nullptr;  // identity payload on the first pass
   for (int i = 0; i < p.passes; ++i) {
     const bool last = i == p.passes - 1;
-    int32_t* kout = last ? sorted_ids : tk[i % 2];
-    int32_t* vout = last ? perm : tv[i % 2];
-    const int nb = 1 << p.bits[i];
+    int32_t* kout = last ? sorted_ids : w.tk[i % 2];
+    int32_t* vout = last ? perm : w.tv[i % 2];
     dim3 grid((unsigned)p.ntiles, (unsigned)B);
-    if (p.tile == 4096)
-      hipLaunchKernelGGL(sort_hist_kernel<4096>, grid, dim3(HT), 0, s, kin, hist,
-                         (int)N, (int)K, p.shift[i], p.bits[i], (int)p.ntiles,
-                         hstride, ctrl);
-    else
-      hipLaunchKernelGGL(sort_hist_kernel<1024>, grid, dim3(HT), 0, s, kin, hist,
-                         (int)N, (int)K, p.shift[i], p.bits[i], (int)p.ntiles,
-                         hstride, ctrl);
-    int rc = check_launch("sort_hist");
-    if (rc) return rc;
-    hipLaunchKernelGGL(sort_scan_kernel, dim3((unsigned)B), dim3(1024), 0, s,
-                       hist, (int64_t)nb * p.ntiles, hstride, ctrl);
-    rc = check_launch("sort_scan");
-    if (rc) return rc;
-    if (p.tile == 4096)
-      hipLaunchKernelGGL(sort_scatter_kernel<4096>, grid, dim3(Geom<4096>::ST), 0,
-                         s, kin, vin, kout, vout, hist, (int)N, (int)K,
-                         p.shift[i], p.bits[i], (int)p.ntiles, hstride, ctrl);
-    else
-      hipLaunchKernelGGL(sort_scatter_kernel<1024>, grid, dim3(Geom<1024>::ST), 0,
-                         s, kin, vin, kout, vout, hist, (int)N, (int)K,
-                         p.shift[i], p.bits[i], (int)p.ntiles, hstride, ctrl);
-    rc = check_launch("sort_scatter");
+    const int32_t* gc = gcur + (size_t)i * 256;
+    uint64_t* st = w.status + (size_t)i * p.ntiles * 256;
+    int32_t* tc = w.tctr + i;
+    switch (p.tile) {
+      case 256:
+        launch_onesweep<256>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
+                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+        break;
+      case 512:
+        launch_onesweep<512>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
+                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+        break;
+      case 1024:
+        launch_onesweep<1024>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
+                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+        break;
+      case 2048:
+        launch_onesweep<2048>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
+                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+        break;
+      default:
+        launch_onesweep<4096>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
+                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+        break;
+    }
+    rc = check_launch("sort_onesweep");
     if (rc) return rc;
     kin = kout;
     vin = vout;
   }
   return FKC_OK;
+}
+
+int label_sort_reset(void* ws, int64_t B, int64_t N, int64_t K,
+                     hipStream_t s) {
+  if (B == 0 || N == 0) return FKC_OK;
+  SortBufs w = carve_sort(ws, B, N, K, nullptr);
+  return launch_fill_i32(w.err, 0, 64 + w.gphase, s);
 }
 
 }  // namespace fkc

@@ -49,6 +49,12 @@ namespace {
 
 constexpr int UR_MAX = 128;  // sorted rows per unit (one wave), at most
 
+// Rows gathered per wave before they are folded (divided by the number of
+// 64-lane column slices per row).
+#ifndef FKC_UPD_RB
+#define FKC_UPD_RB 32
+#endif
+
 // Rows per unit: 128 when that still gives >= 2048 units (512 workgroups),
 // else 64, else 32 — small N needs the extra waves to hide its latency.
 int choose_ur(int64_t B, int64_t N) {
@@ -126,6 +132,7 @@ __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The old row is read only when the shift is wanted.
 template <int DT>
 __device__ inline void finalize_row(const float* row, int cnt,
                                     typename Elem<DT>::T* crow, float* csq,
@@ -134,12 +141,14 @@ __device__ inline void finalize_row(const float* row, int cnt,
   const float fc = (float)cnt;
   float sq = 0.f, sh = 0.f;
   for (int d = lane; d < D; d += 64) {
-    const typename E::T o = crow[d];
     const typename E::T n = E::store(row[d] / fc);
+    const float nf = E::load(n);
+    if (shift != nullptr) {
+      const float df = nf - E::load(crow[d]);
+      sh = fmaf(df, df, sh);
+    }
     crow[d] = n;
-    const float nf = E::load(n), df = nf - E::load(o);
     sq = fmaf(nf, nf, sq);
-    sh = fmaf(df, df, sh);
   }
   sq = wave_sum(sq);
   if (lane == 0) *csq = sq;
@@ -148,6 +157,36 @@ __device__ inline void finalize_row(const float* row, int cnt,
     if (lane == 0)
       atomicMax(reinterpret_cast<unsigned int*>(shift), __float_as_uint(sqrtf(sh)));
   }
+}
+
+// As finalize_row, with the old row already in registers (lane-strided:
+// old[j] holds element lane + 64 j), prefetched when the run started so the
+// flush does not wait for it.  Same arithmetic, same bits.
+template <int DT, int FJ>
+__device__ inline void finalize_row_pref(const float* row, int cnt,
+                                         typename Elem<DT>::T* crow, float* csq,
+                                         float* shift,
+                                         const typename Elem<DT>::T (&old)[FJ],
+                                         int D, int lane) {
+  using E = Elem<DT>;
+  const float fc = (float)cnt;
+  float sq = 0.f, sh = 0.f;
+#pragma unroll
+  for (int j = 0; j < FJ; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) {
+      const typename E::T n = E::store(row[d] / fc);
+      crow[d] = n;
+      const float nf = E::load(n), df = nf - E::load(old[j]);
+      sq = fmaf(nf, nf, sq);
+      sh = fmaf(df, df, sh);
+    }
+  }
+  sq = wave_sum(sq);
+  if (lane == 0) *csq = sq;
+  sh = wave_sum(sh);
+  if (lane == 0)
+    atomicMax(reinterpret_cast<unsigned int*>(shift), __float_as_uint(sqrtf(sh)));
 }
 
 template <int DT, int VEC, int NI, bool INDEXED>
@@ -161,7 +200,8 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
                    FinArgs<typename Elem<DT>::T> fin,
                    const int32_t* __restrict__ ctrl) {
   using T = typename Elem<DT>::T;
-  constexpr int RB = 32 / NI;  // rows in flight per wave
+  constexpr int RB = FKC_UPD_RB / NI;  // rows in flight per wave
+  constexpr int FJ = VEC * NI;  // fused finalize: D <= 64 * VEC * NI
   __shared__ float fin_row[UT / 64][FIN_DMAX];
   if (loop_done(ctrl)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -174,6 +214,18 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   const int p1 = min(p0 + ur, N);
 
   const bool fused = fin.cent != nullptr;  // uniform
+  // With the shift wanted, the old centroid row of each run's label is
+  // loaded when the run starts (the label's row is finalized, if here, only
+  // by this wave: a label is one contiguous run).
+  const bool pref = fused && fin.shift != nullptr;  // uniform
+  T oldv[FJ];
+  auto prefetch_old = [&](int id) {
+    if (!pref || (uint32_t)id >= (uint32_t)K) return;
+    const T* crow = fin.cent + ((size_t)b * K + id) * D;
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
+      if (lane + 64 * j < D) oldv[j] = crow[lane + 64 * j];
+  };
   const int32_t* ib = sids + (size_t)b * N;
   const int32_t* pb = INDEXED ? perm + (size_t)b * N : nullptr;
   const T* xb = x + (size_t)b * N * D;
@@ -248,8 +300,13 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
           for (int v = 0; v < VEC; ++v) r[col[i] + v] = acc[i][v];
         }
       wave_lds_sync();
-      finalize_row<DT>(r, e - s, fin.cent + ((size_t)b * K + id) * D,
-                       fin.c_sq + (size_t)b * K + id, fin.shift, D, lane);
+      if (pref)
+        finalize_row_pref<DT, FJ>(r, e - s, fin.cent + ((size_t)b * K + id) * D,
+                                  fin.c_sq + (size_t)b * K + id, fin.shift,
+                                  oldv, D, lane);
+      else
+        finalize_row<DT>(r, e - s, fin.cent + ((size_t)b * K + id) * D,
+                         fin.c_sq + (size_t)b * K + id, nullptr, D, lane);
     } else if ((uint32_t)id < (uint32_t)K) {
       float* dst = sb + (size_t)id * D;
 #pragma unroll
@@ -285,6 +342,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
 
   int cur = __builtin_amdgcn_readfirstlane(ivs[0]);
   int rs = p0;
+  prefetch_old(cur);
   if (overwrite && !fused && !(has_prev && prev == cur))
     zero_bins(has_prev ? prev + 1 : 0, cur);
 
@@ -321,6 +379,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
             if (overwrite && !fused) zero_bins(cur + 1, id);
             cur = id;
             rs = base + j;
+            prefetch_old(cur);
 #pragma unroll
             for (int i = 0; i < NI; ++i)
 #pragma unroll

@@ -62,6 +62,34 @@ def test_label_sort_zipf_skew():
     assert np.array_equal(_np(p), ep) and np.array_equal(_np(s), es)
 
 
+@pytest.mark.parametrize("tile", [256, 512, 1024, 2048, 4096])
+@pytest.mark.parametrize("B,N,K,pattern", [
+    (2, 100000, 8192, "random"), (1, 70001, 70000, "random"),
+    (1, 300000, 4096, "same"), (3, 9000, 9000, "descending"),
+])
+def test_label_sort_every_tile_size(monkeypatch, tile, B, N, K, pattern):
+    """Each tile size of the single-sweep passes (FKC_SORT_TILE), over
+    random, all-equal and strictly descending labels (every tile then waits
+    on its predecessors for every digit), bit-exact against the stable sort;
+    each case is sorted twice in a row (the caching allocator then usually
+    hands the second call the first call's workspace memory, counters and
+    status words included)."""
+    from flash_kmeans_cuda.ops import label_sort
+    monkeypatch.setenv("FKC_SORT_TILE", str(tile))
+    rng = np.random.default_rng(tile + N)
+    if pattern == "random":
+        ids = rng.integers(-2, K + 2, (B, N)).astype(np.int32)
+    elif pattern == "same":
+        ids = np.full((B, N), K - 1, np.int32)
+    else:
+        ids = np.broadcast_to(np.arange(N - 1, -1, -1, dtype=np.int32) % K, (B, N)).copy()
+    es, ep = O.label_sort(ids, K)
+    for _ in range(2):
+        s, p = label_sort(_t(ids), K)
+        assert np.array_equal(_np(p), ep)
+        assert np.array_equal(_np(s), es)
+
+
 def _update_case(B, N, K, D, dtype, seed, invalid=False, zipf=False):
     rng = np.random.default_rng(seed)
     x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
