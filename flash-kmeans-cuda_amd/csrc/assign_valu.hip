@@ -143,12 +143,16 @@ row_sqnorm_kernel(const typename Elem<DT>::T* __restrict__ src,
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const typename E::T* r = src + row * D;
+  // Column order and reduction shared with the finalize kernels.
+  const int vec = row_vec(D);
   float acc = 0.f;
-  for (int d = lane; d < D; d += 64) {
-    const float v = E::load(r[d]);
-    acc = fmaf(v, v, acc);
+  for (int c = vec * lane; c < D; c += vec * 64) {
+    for (int v = 0; v < vec; ++v) {
+      const float f = E::load(r[c + v]);
+      acc = fmaf(f, f, acc);
+    }
   }
-  acc = wave_sum(acc);
+  acc = row_sum(acc);
   if (lane == 0) out[row] = acc;
 }
 

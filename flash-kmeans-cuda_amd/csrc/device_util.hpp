@@ -50,6 +50,36 @@ __device__ inline int wave_sum_i(int v) {
   return v;
 }
 
+// Row reductions of the norm / finalize kernels (row_sqnorm, finalize, the
+// finalize fused into the centroid update) all use one order, so their
+// results agree bit for bit: lane l covers the columns VEC*(l + 64*i) + v,
+// i = 0, 1, ..., v < VEC, with VEC = row_vec(D) (2 for even D, else 1),
+// accumulated with fma in (i, v) order; the 64 lane partials are then added
+// by row_sum.  (The centroid update holds its sums in exactly this layout.)
+__host__ __device__ inline int row_vec(int D) { return (D & 1) ? 1 : 2; }
+
+// Sum of v over the 64 lanes by a fixed tree of DPP moves: pairs and quads
+// (quad_perm), 8-lane halves (row_half_mirror), 16-lane rows (row_mirror),
+// then rows 0+1 and 2+3 (row_bcast:15) and all four rows (row_bcast:31).
+// The total lands in lane 63 and is returned to every lane.  Each step is
+// one DPP add (the butterfly of __shfl_xor costs an LDS-crossbar round trip
+// per step).
+__device__ inline float row_sum(float v) {
+#define FKC_DPP_ADD(CTRL, RMASK)                                             \
+  v += __builtin_bit_cast(                                                   \
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, \
+                                         RMASK, 0xF, false))
+  FKC_DPP_ADD(0xB1, 0xF);   // quad_perm [1,0,3,2]
+  FKC_DPP_ADD(0x4E, 0xF);   // quad_perm [2,3,0,1]
+  FKC_DPP_ADD(0x141, 0xF);  // row_half_mirror
+  FKC_DPP_ADD(0x140, 0xF);  // row_mirror
+  FKC_DPP_ADD(0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+  FKC_DPP_ADD(0x143, 0xC);  // row_bcast:31 into rows 2 and 3
+#undef FKC_DPP_ADD
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // Number of set bits of `mask` in lanes below the calling lane.
 __device__ inline uint32_t lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(

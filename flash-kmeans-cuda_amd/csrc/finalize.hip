@@ -34,21 +34,27 @@ finalize_kernel(const float* __restrict__ sums,
   const float* sr = sums + row * D;
   const typename E::T* orow = old + row * D;
   typename E::T* nrow = out + row * D;
+  // Column order and reduction shared with row_sqnorm and the finalize
+  // fused into the centroid update.
+  const int vec = row_vec(D);
   float sq = 0.f, sh = 0.f;
-  for (int d = lane; d < D; d += 64) {
-    const typename E::T o = orow[d];
-    const typename E::T n = cnt > 0 ? E::store(sr[d] / fc) : o;
-    nrow[d] = n;
-    const float nf = E::load(n), df = nf - E::load(o);
-    sq = fmaf(nf, nf, sq);
-    sh = fmaf(df, df, sh);
+  for (int c = vec * lane; c < D; c += vec * 64) {
+    for (int v = 0; v < vec; ++v) {
+      const int d = c + v;
+      const typename E::T o = orow[d];
+      const typename E::T n = cnt > 0 ? E::store(sr[d] / fc) : o;
+      nrow[d] = n;
+      const float nf = E::load(n), df = nf - E::load(o);
+      sq = fmaf(nf, nf, sq);
+      sh = fmaf(df, df, sh);
+    }
   }
   if (c_sq_out != nullptr) {
-    sq = wave_sum(sq);
+    sq = row_sum(sq);
     if (lane == 0) c_sq_out[row] = sq;
   }
   if (shift_out != nullptr) {
-    sh = wave_sum(sh);
+    sh = row_sum(sh);
     if (lane == 0)
       atomicMax(reinterpret_cast<unsigned int*>(shift_out),
                 __float_as_uint(sqrtf(sh)));

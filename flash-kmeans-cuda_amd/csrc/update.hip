@@ -49,15 +49,12 @@ namespace {
 
 constexpr int UR_MAX = 128;  // sorted rows per unit (one wave), at most
 
-// Rows gathered per wave before they are folded (divided by the number of
-// 64-lane column slices per row).
-#ifndef FKC_UPD_RB
-#define FKC_UPD_RB 32
-#endif
-
 // Rows per unit: 128 when that still gives >= 2048 units (512 workgroups),
 // else 64, else 32 — small N needs the extra waves to hide its latency.
 int choose_ur(int64_t B, int64_t N) {
+#ifdef FKC_UR_FORCE
+  return FKC_UR_FORCE;
+#endif
   for (int ur = UR_MAX; ur > 32; ur >>= 1)
     if (B * ((N + ur - 1) / ur) >= 2048) return ur;
   return 32;
@@ -74,6 +71,13 @@ struct RawCols<FKC_F32, VEC> {
   using T = typename std::conditional<VEC == 2, float2, float>::type;
   __device__ static T load(const float* p) { return *reinterpret_cast<const T*>(p); }
   __device__ static T zero() { return T{}; }
+  // Store VEC elements as one access.
+  __device__ static void store(float* p, const float* e) {
+    if constexpr (VEC == 2)
+      *reinterpret_cast<float2*>(p) = float2{e[0], e[1]};
+    else
+      *p = e[0];
+  }
   __device__ static void cvt(T r, float* out) {
     if constexpr (VEC == 2) {
       out[0] = r.x;
@@ -91,6 +95,17 @@ struct RawCols {  // 16-bit element types
     return *reinterpret_cast<const T*>(p);
   }
   __device__ static T zero() { return 0; }
+  // Store VEC elements as one access.
+  __device__ static void store(typename E::T* p, const typename E::T* e) {
+    uint32_t bits = 0;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      uint16_t h;
+      __builtin_memcpy(&h, &e[v], 2);
+      bits |= (uint32_t)h << (16 * v);
+    }
+    *reinterpret_cast<T*>(p) = (T)bits;
+  }
   __device__ static void cvt(T r, float* out) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
@@ -106,16 +121,17 @@ struct UnitMeta {  // per unit, int32 x 4
   enum { TAIL_ID = 0, TAIL_LEN = 1, HEAD_LEN = 2, THROUGH = 3 };
 };
 
-constexpr int FIN_DMAX = 512;  // widest row the fused finalize stages in LDS
+constexpr int FIN_DMAX = 512;  // widest row the fused finalize handles
 
 // Finalize fused into the update (the Lloyd loop): where a bin's final sum
 // is known, the wave that holds it computes the new centroid row at once,
 // exactly as finalize_kernel (finalize.hip) would from the stored sums:
 // new = cast(sum / count) with IEEE division, c_sq = sum of new^2 and the
-// row's shift ||new - old||_2, both accumulated lane-strided (d = lane,
-// lane+64, ...) in fma order and reduced by wave_sum, so every bit matches
-// the separate kernel.  The row's sums come from LDS (`row`).  Empty bins
-// are left alone: their centroid, c_sq and zero shift stand.
+// row's shift ||new - old||_2, accumulated in the column order shared with
+// finalize_kernel and row_sqnorm (lane l: columns VEC*(l + 64 i) + v, fma in
+// (i, v) order) and added over lanes by row_sum, so every bit matches the
+// separate kernels.  Empty bins are left alone: their centroid, c_sq and
+// zero shift stand.
 template <typename T>
 struct FinArgs {
   T* cent;          // (B, K, D) centroids, updated in place; null: not fused
@@ -132,61 +148,43 @@ __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// The old row is read only when the shift is wanted.
+// c_sq and (when wanted) the shift of a finalized row from the lanes'
+// partial sums.
+__device__ inline void finish_norms(float sq, float sh, float* csq,
+                                    float* shift, int lane) {
+  sq = row_sum(sq);
+  if (lane == 0) *csq = sq;
+  if (shift != nullptr) {
+    sh = row_sum(sh);
+    if (lane == 0)
+      atomicMax(reinterpret_cast<unsigned int*>(shift), __float_as_uint(sqrtf(sh)));
+  }
+}
+
+// Finalize from a row of sums in LDS (the run merge).  The old row is read
+// only when the shift is wanted.
 template <int DT>
 __device__ inline void finalize_row(const float* row, int cnt,
                                     typename Elem<DT>::T* crow, float* csq,
                                     float* shift, int D, int lane) {
   using E = Elem<DT>;
   const float fc = (float)cnt;
+  const int vec = row_vec(D);
   float sq = 0.f, sh = 0.f;
-  for (int d = lane; d < D; d += 64) {
-    const typename E::T n = E::store(row[d] / fc);
-    const float nf = E::load(n);
-    if (shift != nullptr) {
-      const float df = nf - E::load(crow[d]);
-      sh = fmaf(df, df, sh);
-    }
-    crow[d] = n;
-    sq = fmaf(nf, nf, sq);
-  }
-  sq = wave_sum(sq);
-  if (lane == 0) *csq = sq;
-  if (shift != nullptr) {
-    sh = wave_sum(sh);
-    if (lane == 0)
-      atomicMax(reinterpret_cast<unsigned int*>(shift), __float_as_uint(sqrtf(sh)));
-  }
-}
-
-// As finalize_row, with the old row already in registers (lane-strided:
-// old[j] holds element lane + 64 j), prefetched when the run started so the
-// flush does not wait for it.  Same arithmetic, same bits.
-template <int DT, int FJ>
-__device__ inline void finalize_row_pref(const float* row, int cnt,
-                                         typename Elem<DT>::T* crow, float* csq,
-                                         float* shift,
-                                         const typename Elem<DT>::T (&old)[FJ],
-                                         int D, int lane) {
-  using E = Elem<DT>;
-  const float fc = (float)cnt;
-  float sq = 0.f, sh = 0.f;
-#pragma unroll
-  for (int j = 0; j < FJ; ++j) {
-    const int d = lane + 64 * j;
-    if (d < D) {
+  for (int c = vec * lane; c < D; c += vec * 64) {
+    for (int v = 0; v < vec; ++v) {
+      const int d = c + v;
       const typename E::T n = E::store(row[d] / fc);
+      const float nf = E::load(n);
+      if (shift != nullptr) {
+        const float df = nf - E::load(crow[d]);
+        sh = fmaf(df, df, sh);
+      }
       crow[d] = n;
-      const float nf = E::load(n), df = nf - E::load(old[j]);
       sq = fmaf(nf, nf, sq);
-      sh = fmaf(df, df, sh);
     }
   }
-  sq = wave_sum(sq);
-  if (lane == 0) *csq = sq;
-  sh = wave_sum(sh);
-  if (lane == 0)
-    atomicMax(reinterpret_cast<unsigned int*>(shift), __float_as_uint(sqrtf(sh)));
+  finish_norms(sq, sh, csq, shift, lane);
 }
 
 template <int DT, int VEC, int NI, bool INDEXED>
@@ -200,11 +198,11 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
                    FinArgs<typename Elem<DT>::T> fin,
                    const int32_t* __restrict__ ctrl) {
   using T = typename Elem<DT>::T;
-  constexpr int RB = FKC_UPD_RB / NI;  // rows in flight per wave
-  constexpr int FJ = VEC * NI;  // fused finalize: D <= 64 * VEC * NI
-  __shared__ float fin_row[UT / 64][FIN_DMAX];
+  using E = Elem<DT>;
+  using RC = RawCols<DT, VEC>;
   if (loop_done(ctrl)) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
   const int b = blockIdx.y;
   const int u = blockIdx.x * (UT / 64) + wave;
   if (u >= nunits) return;
@@ -218,14 +216,6 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   // loaded when the run starts (the label's row is finalized, if here, only
   // by this wave: a label is one contiguous run).
   const bool pref = fused && fin.shift != nullptr;  // uniform
-  T oldv[FJ];
-  auto prefetch_old = [&](int id) {
-    if (!pref || (uint32_t)id >= (uint32_t)K) return;
-    const T* crow = fin.cent + ((size_t)b * K + id) * D;
-#pragma unroll
-    for (int j = 0; j < FJ; ++j)
-      if (lane + 64 * j < D) oldv[j] = crow[lane + 64 * j];
-  };
   const int32_t* ib = sids + (size_t)b * N;
   const int32_t* pb = INDEXED ? perm + (size_t)b * N : nullptr;
   const T* xb = x + (size_t)b * N * D;
@@ -245,12 +235,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     cok[i] = col[i] < D;  // D % VEC == 0, so the whole vector is in range
   }
 
-  float acc[NI][VEC];
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[i][v] = 0.f;
-
+  using Acc = float[NI][VEC];
   int tail_id = 0, tail_len = 0, head_len = 0, through = 0;
 
   // Zero sums/counts of bins [lo, hi) (overwrite mode only).
@@ -269,44 +254,55 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
       for (int k = lo + lane; k < hi; k += 64) cntb[k] = 0;
   };
 
-  auto store_part = [&](int slot) {
+  auto store_part = [&](int slot, const Acc& a) {
     float* dst = partb + ((size_t)u * 2 + slot) * D;
 #pragma unroll
     for (int i = 0; i < NI; ++i)
       if (cok[i]) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) dst[col[i] + v] = acc[i][v];
+        for (int v = 0; v < VEC; ++v) dst[col[i] + v] = a[i][v];
       }
   };
 
-  // Close the run of label `id` covering sorted rows [s, e).
-  auto flush = [&](int id, int s, int e) {
+  // Close the run of label `id` covering sorted rows [s, e) with sums `a`.
+  auto flush = [&](int id, int s, int e, const Acc& a) {
     const bool continuing = s == p0 && has_prev && prev == id;
     const bool continued = e == p1 && has_next && next == id;
     if (continuing) {
-      store_part(0);
+      store_part(0, a);
       head_len = e - s;
       through = continued ? 1 : 0;
     } else if (continued) {
-      store_part(1);
+      store_part(1, a);
       tail_id = id;
       tail_len = e - s;
     } else if (fused && (uint32_t)id < (uint32_t)K) {
-      float* r = fin_row[wave];
+      // The run's sums are in the shared column order (the fused path has
+      // one column block, so col[i] = VEC*(lane + 64 i)): finalize straight
+      // from them.  The old row is read only when the shift is wanted.
+      const float fc = (float)(e - s);
+      T* crow = fin.cent + ((size_t)b * K + id) * D;
+      float sq = 0.f, sh = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i)
         if (cok[i]) {
+          float of[VEC];
+          if (pref) RC::cvt(RC::load(crow + col[i]), of);
+          T nv[VEC];
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) r[col[i] + v] = acc[i][v];
+          for (int v = 0; v < VEC; ++v) {
+            nv[v] = E::store(a[i][v] / fc);
+            const float nf = E::load(nv[v]);
+            sq = fmaf(nf, nf, sq);
+            if (pref) {
+              const float df = nf - of[v];
+              sh = fmaf(df, df, sh);
+            }
+          }
+          RC::store(crow + col[i], nv);
         }
-      wave_lds_sync();
-      if (pref)
-        finalize_row_pref<DT, FJ>(r, e - s, fin.cent + ((size_t)b * K + id) * D,
-                                  fin.c_sq + (size_t)b * K + id, fin.shift,
-                                  oldv, D, lane);
-      else
-        finalize_row<DT>(r, e - s, fin.cent + ((size_t)b * K + id) * D,
-                         fin.c_sq + (size_t)b * K + id, nullptr, D, lane);
+      finish_norms(sq, sh, fin.c_sq + (size_t)b * K + id,
+                   pref ? fin.shift : nullptr, lane);
     } else if ((uint32_t)id < (uint32_t)K) {
       float* dst = sb + (size_t)id * D;
 #pragma unroll
@@ -315,9 +311,9 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             if (overwrite)
-              dst[col[i] + v] = acc[i][v];
+              dst[col[i] + v] = a[i][v];
             else
-              dst[col[i] + v] += acc[i][v];
+              dst[col[i] + v] += a[i][v];
           }
         }
       if (lead && lane == 0) {
@@ -330,7 +326,8 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   };
 
   // Labels and permutation entries of the unit's rows, one per lane per
-  // 64-row chunk, loaded up front.
+  // 64-row chunk, loaded up front, and per chunk the mask of rows that start
+  // a new run (never the unit's first row: its run is open from the start).
   constexpr int CH = UR_MAX / 64;
   int ivs[CH], pvs[CH];
 #pragma unroll
@@ -339,64 +336,114 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     ivs[c] = p < p1 ? ib[p] : 0;
     pvs[c] = INDEXED ? (p < p1 ? pb[p] : 0) : p;
   }
+  uint64_t starts[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    int before = __shfl_up(ivs[c], 1, 64);
+    if (lane == 0)
+      before = c == 0 ? ivs[0] : __builtin_amdgcn_readlane(ivs[c - 1], 63);
+    const int p = p0 + c * 64 + lane;
+    starts[c] = __builtin_amdgcn_ballot_w64(p < p1 && ivs[c] != before);
+  }
 
   int cur = __builtin_amdgcn_readfirstlane(ivs[0]);
   int rs = p0;
-  prefetch_old(cur);
   if (overwrite && !fused && !(has_prev && prev == cur))
     zero_bins(has_prev ? prev + 1 : 0, cur);
 
-  using R = typename RawCols<DT, VEC>::T;
+  // Rows are gathered RB at a time (raw words in flight, converted when
+  // folded) and folded in sub-batches of FH rows.  The fold is straight-line
+  // code with no branch: at every row the running sums go to an LDS slot
+  // (the next free slot when the row starts a run, else a scratch slot) and
+  // restart from zero if the row starts a run.  The runs that closed in the
+  // sub-batch are then flushed from their slots by a loop with a single
+  // flush site.  (A per-row branch to a flush, even one that is rarely
+  // taken, doubled the kernel's time.)
+  constexpr int RB = 32 / NI;          // rows in flight per wave
+  constexpr int FH = 16 / NI;          // rows per folded sub-batch
+  constexpr int SL = NI * VEC;         // floats per lane per slot
+  __shared__ float slot[UT / 64][FH + 1][SL][64];
+  float (*wslot)[SL][64] = slot[wave];
+  const int urows = p1 - p0;
+  Acc acc;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int base = p0 + c * 64;
-    if (base >= p1) break;
-    const int nrow = min(64, p1 - base);
-    const int iv = ivs[c], pv = pvs[c];
-    for (int j0 = 0; j0 < nrow; j0 += RB) {
-      // RB rows in flight: raw column words first, conversion when folded.
-      R raw[RB][NI];
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int jj = 0; jj < RB; ++jj) {
-        const int j = j0 + jj;
-        const int row = __builtin_amdgcn_readlane(pv, j < nrow ? j : 0);
-        // A permutation entry outside [0,N), or a row past the unit, reads
-        // nothing and contributes zeros.
-        const bool rok = j < nrow && (uint32_t)row < (uint32_t)N;
-        const T* xr = xb + (size_t)(rok ? row : 0) * D;
+    for (int v = 0; v < VEC; ++v) acc[i][v] = 0.f;
+
+  using R = typename RC::T;
+#pragma unroll
+  for (int q = 0; q < UR_MAX / RB; ++q) {
+    const int r0 = q * RB;  // first unit row of the batch
+    if (r0 >= urows) break;
+    R raw[RB][NI];
+    uint32_t okm = 0;  // rows with a permutation entry in [0,N) inside the unit
+#pragma unroll
+    for (int jj = 0; jj < RB; ++jj) {
+      const int r = r0 + jj;
+      const int rr = min(r, urows - 1);
+      const int row = __builtin_amdgcn_readlane(rr < 64 ? pvs[0] : pvs[CH - 1], rr & 63);
+      // A permutation entry outside [0,N), or a row past the unit, reads
+      // row 0 and is not folded.
+      const bool rok = r < urows && (uint32_t)row < (uint32_t)N;
+      okm |= rok ? (1u << jj) : 0u;
+      const T* xr = xb + (size_t)(rok ? row : 0) * D;
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        raw[jj][i] = cok[i] ? RC::load(xr + col[i]) : RC::zero();
+    }
+#pragma unroll
+    for (int h = 0; h < RB / FH; ++h) {
+      const int s0 = r0 + h * FH;  // first unit row of the sub-batch
+      if (s0 >= urows) break;
+      const uint64_t cm = starts[s0 >> 6] >> (s0 & 63);
+      const uint32_t hb = (uint32_t)cm & ((1u << FH) - 1u);  // run starts
+      int nseg = 0;
+#pragma unroll
+      for (int t = 0; t < FH; ++t) {
+        const int jj = h * FH + t;
+        const bool st = (hb >> t) & 1u;  // wave-uniform
+        const int sl = st ? nseg : FH;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-          raw[jj][i] = (cok[i] && rok) ? RawCols<DT, VEC>::load(xr + col[i])
-                                       : RawCols<DT, VEC>::zero();
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) wslot[sl][i * VEC + v][lane] = acc[i][v];
+        nseg += st ? 1 : 0;
+        const bool use = (okm >> jj) & 1u;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          float f[VEC];
+          RC::cvt(raw[jj][i], f);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            const float base = st ? 0.f : acc[i][v];
+            acc[i][v] = use ? base + f[v] : base;
+          }
+        }
       }
+      if (hb != 0u) {
+        wave_lds_sync();
+        uint32_t m = hb;
+#pragma unroll 1
+        for (int k = 0; m != 0u; ++k) {
+          const int t = __builtin_ctz(m);
+          m &= m - 1u;
+          const int r = s0 + t;  // unit row where the next run starts
+          Acc a;
 #pragma unroll
-      for (int jj = 0; jj < RB; ++jj) {
-        const int j = j0 + jj;
-        if (j < nrow) {
-          const int id = __builtin_amdgcn_readlane(iv, j);
-          if (id != cur) {
-            flush(cur, rs, base + j);
-            if (overwrite && !fused) zero_bins(cur + 1, id);
-            cur = id;
-            rs = base + j;
-            prefetch_old(cur);
+          for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int i = 0; i < NI; ++i)
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[i][v] = 0.f;
-          }
-#pragma unroll
-          for (int i = 0; i < NI; ++i) {
-            float f[VEC];
-            RawCols<DT, VEC>::cvt(raw[jj][i], f);
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) acc[i][v] += f[v];
-          }
+            for (int v = 0; v < VEC; ++v) a[i][v] = wslot[k][i * VEC + v][lane];
+          flush(cur, rs, p0 + r, a);
+          const int id = __builtin_amdgcn_readlane(r < 64 ? ivs[0] : ivs[CH - 1], r & 63);
+          if (overwrite && !fused) zero_bins(cur + 1, id);
+          cur = id;
+          rs = p0 + r;
         }
       }
     }
   }
-  flush(cur, rs, p1);
+  flush(cur, rs, p1, acc);
   if (overwrite && !fused && !has_next) zero_bins(cur + 1, K);
 
   if (lead && lane == 0) {

@@ -174,10 +174,13 @@ FKC_CAPI int fkc_kmeans_lloyd(const void* x, void* centroids,
                               int32_t* n_iters_dev, int32_t* n_iters_host);
 
 /*
- * Profiling hook for benchmarks (no counterpart in the reference): when
- * enabled, fkc_kmeans_lloyd brackets every assignment launch with HIP events
- * on its stream.  fkc_profile_assign_ms() synchronises on the recorded events
- * and returns the summed assignment time in ms and the launch count.
+ * Profiling hook for benchmarks (no counterpart in the reference): with
+ * enable = k > 0, fkc_kmeans_lloyd times the assignment launch of every k-th
+ * loop iteration (iterations 0, k, 2k, ...) with HIP events stamped by the
+ * launch's dispatch on its stream (each timed launch costs the stream a few
+ * microseconds, so k > 1 keeps that out of most iterations); enable = 0
+ * turns it off.  fkc_profile_assign_ms() synchronises on the recorded events
+ * and returns the summed assignment time in ms and the timed launch count.
  */
 FKC_CAPI void fkc_profile_enable(int enable);
 FKC_CAPI int fkc_profile_assign_ms(double* total_ms, int64_t* launches);
