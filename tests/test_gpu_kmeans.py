@@ -232,6 +232,27 @@ def test_fused_loop_equals_per_op_path_across_widths(D, dtype):
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
+@pytest.mark.parametrize("B,N,K,D,dtype", [
+    (1, 20000, 300, 128, "f16"),    # 2 sort passes
+    (3, 10000, 256, 64, "bf16"),    # 1 sort pass (labels from the assign skip the sentinel bin)
+    (2, 30000, 2000, 32, "bf16"),   # 32-feature direct stages
+    (1, 80000, 70000, 16, "f16"),   # 3 sort passes
+])
+def test_loop_sort_digit_counts(B, N, K, D, dtype):
+    """The loop's label sort alternates two state phases over iterations
+    (digit counts, tile status words, tile counters) and clears them once
+    per call; the per-op path runs standalone sorts.  Both must agree bit
+    for bit over 3 iterations, for 1, 2 and 3 sort passes."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    rng = np.random.default_rng(K + D)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    init = np.ascontiguousarray(x[:, :K])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it, verbose=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 def test_deterministic_loop():
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c3"]
