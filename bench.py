@@ -23,7 +23,7 @@ Reported:
   ms_per_iter_ref_method  one whole call with max_iters=1 (README.md:221 of
                         the reference)
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c5]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--config c5]
        python bench.py --report        per-config table (c1..c5): assign TFLOPS,
                                        ms/iter (steady state and one-iteration
                                        call), roofline fraction ideal/measured
@@ -263,8 +263,12 @@ def _report(configs) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 50 warm-up iterations (~45 ms of load at c5): the GPU's power
+    # management settles within ~20 iterations of sustained load; with 3, the
+    # first ~15 timed iterations ran up to 15% slower (assign 0.92 vs 0.80 ms
+    # per launch on the same box).
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="c5")
     ap.add_argument("--cpu-sample", type=int, default=131072)
     ap.add_argument("--no-cpu-baseline", action="store_true")
