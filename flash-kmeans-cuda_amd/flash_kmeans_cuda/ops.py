@@ -64,10 +64,14 @@ def euclid_assign(
     return _C.euclid_assign(x, centroids, x_sq, c_sq, out)
 
 
-def label_sort(cluster_ids: torch.Tensor, K: int) -> Tuple[torch.Tensor, torch.Tensor]:
+def label_sort(cluster_ids: torch.Tensor, K: int, *,
+               workspace: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Stable sort of (B, N) int32 labels along N -> (sorted_ids, perm) int32.
 
     Labels outside [0, K) sort after every valid label, in index order.
+    workspace: optional caller-owned uint8 CUDA tensor of at least
+    fkc_label_sort_workspace_bytes(B, N, K) bytes, 256-byte aligned; its first
+    int32 is the sort's health word (nonzero after the call: invalid output).
     """
     cluster_ids = _ensure_contig(cluster_ids, "cluster_ids")
     if cluster_ids.dtype != torch.int32:
@@ -75,8 +79,15 @@ def label_sort(cluster_ids: torch.Tensor, K: int) -> Tuple[torch.Tensor, torch.T
     B, N = cluster_ids.shape
     sorted_ids = torch.empty_like(cluster_ids)
     perm = torch.empty_like(cluster_ids)
-    ws = _lib.workspace(_lib.lib.fkc_label_sort_workspace_bytes(B, N, K),
-                        cluster_ids.device)
+    need = _lib.lib.fkc_label_sort_workspace_bytes(B, N, K)
+    if workspace is None:
+        ws = _lib.workspace(need, cluster_ids.device)
+    else:
+        if (workspace.dtype != torch.uint8 or not workspace.is_contiguous()
+                or workspace.device != cluster_ids.device or workspace.numel() < need):
+            raise ValueError(f"label_sort: workspace must be a contiguous uint8 tensor of "
+                             f">= {need} bytes on {cluster_ids.device}")
+        ws = workspace
     _lib.check(_lib.lib.fkc_label_sort(
         cluster_ids.data_ptr(), sorted_ids.data_ptr(), perm.data_ptr(), B, N, K,
         ws.data_ptr(), ws.numel(), _lib.stream_of(cluster_ids)), "label_sort")

@@ -90,6 +90,10 @@ FKC_CAPI int fkc_row_sqnorm(const void* src, float* out, int64_t rows,
  * order.  Labels outside [0,K) sort after every valid label, in index order.
  * Replaces torch.sort(cluster_ids, dim=1) at ops.py:89 (the reference asks
  * stable=False; this sort is always stable).
+ * The workspace's first int32 is the sort's health word, cleared by every
+ * call: nonzero after the call completes means a workgroup of a pass gave up
+ * waiting for its predecessors' tile counts (a bounded wait that never
+ * expires in a correct run) and the output is not valid.
  */
 FKC_CAPI size_t fkc_label_sort_workspace_bytes(int64_t B, int64_t N,
                                                int64_t K);

@@ -39,6 +39,19 @@ SORT_CASES = [
 ]
 
 
+def _sort_ws(B, N, K):
+    """A label-sort workspace the test can inspect (health word = int32 0)."""
+    from flash_kmeans_cuda import _lib
+    n = _lib.lib.fkc_label_sort_workspace_bytes(B, N, K)
+    ws = torch.full((n,), 0xA5, dtype=torch.uint8, device="cuda")  # stale bytes
+    return ws
+
+
+def _health(ws):
+    torch.cuda.synchronize()
+    return int(ws[:4].view(torch.int32).item())
+
+
 @pytest.mark.parametrize("B,N,K", SORT_CASES)
 def test_label_sort_bit_exact(B, N, K):
     from flash_kmeans_cuda.ops import label_sort
@@ -46,10 +59,12 @@ def test_label_sort_bit_exact(B, N, K):
     ids = rng.integers(0, K, (B, N)).astype(np.int32)
     if N > 50:
         ids[:, rng.integers(0, N, N // 50)] = rng.integers(-3, 2 * K + 3, (B, N // 50))
-    s, p = label_sort(_t(ids), K)
+    ws = _sort_ws(B, N, K)
+    s, p = label_sort(_t(ids), K, workspace=ws)
     es, ep = O.label_sort(ids, K)
     assert np.array_equal(_np(p), ep)
     assert np.array_equal(_np(s), es)
+    assert _health(ws) == 0
 
 
 def test_label_sort_zipf_skew():
@@ -71,9 +86,9 @@ def test_label_sort_every_tile_size(monkeypatch, tile, B, N, K, pattern):
     """Each tile size of the single-sweep passes (FKC_SORT_TILE), over
     random, all-equal and strictly descending labels (every tile then waits
     on its predecessors for every digit), bit-exact against the stable sort;
-    each case is sorted twice in a row (the caching allocator then usually
-    hands the second call the first call's workspace memory, counters and
-    status words included)."""
+    each case is sorted twice in a row on one workspace that starts out
+    filled with stale bytes (the second call finds the first call's counters
+    and status words), and the sort's health word stays 0."""
     from flash_kmeans_cuda.ops import label_sort
     monkeypatch.setenv("FKC_SORT_TILE", str(tile))
     rng = np.random.default_rng(tile + N)
@@ -84,10 +99,12 @@ def test_label_sort_every_tile_size(monkeypatch, tile, B, N, K, pattern):
     else:
         ids = np.broadcast_to(np.arange(N - 1, -1, -1, dtype=np.int32) % K, (B, N)).copy()
     es, ep = O.label_sort(ids, K)
+    ws = _sort_ws(B, N, K)
     for _ in range(2):
-        s, p = label_sort(_t(ids), K)
+        s, p = label_sort(_t(ids), K, workspace=ws)
         assert np.array_equal(_np(p), ep)
         assert np.array_equal(_np(s), es)
+        assert _health(ws) == 0
 
 
 def _update_case(B, N, K, D, dtype, seed, invalid=False, zipf=False):
