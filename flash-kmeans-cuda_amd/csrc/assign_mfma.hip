@@ -32,7 +32,8 @@
 // Feature widths that are not a multiple of 32 are zero-padded in registers
 // and LDS (zeros add nothing to a dot product).
 //
-// Workgroup: 4 waves x PT point tiles x 16 points (PT chosen per grid size).
+// Workgroup: 4 waves x PT point tiles x 16 points (PT chosen per grid size;
+// PT = 8 at D = 128 on large grids: 128 point registers, 2 waves per SIMD).
 // Centroids pass through LDS in double-buffered stages with one barrier per
 // stage; the next stage's loads are in flight while the matrix cores work
 // on the current one.  For D = 32, 64, 128 and 256 the stages are direct
@@ -59,7 +60,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // shapes): FKC_AB, minimum waves per SIMD asked of the register allocator
 // for the lighter variants; FKC_EXACT_MAX_K, largest K that tracks the exact
 // index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
-// FKC_KC_DMA, centroid rows per direct stage (D <= 128); FKC_SCHED_GROUPS,
+// FKC_KC_DMA, centroid rows per direct stage (D <= 128); FKC_KC_DMA8, the
+// same for the eight-tile variant (two workgroups per CU leave it twice the
+// LDS); FKC_SCHED_GROUPS,
 // LDS-read / MFMA / VALU ordering hints in the direct-stage loop.
 #ifndef FKC_AB
 #define FKC_AB 2
@@ -72,6 +75,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #endif
 #ifndef FKC_KC_DMA
 #define FKC_KC_DMA 64
+#endif
+#ifndef FKC_KC_DMA8
+#define FKC_KC_DMA8 128
 #endif
 #ifndef FKC_SCHED_GROUPS
 #define FKC_SCHED_GROUPS 1
@@ -136,7 +142,10 @@ __device__ inline void fold_exact(const f32x4& acc, float& best, int& bidx,
 // the exact index in the loop instead of re-scoring at the end.  D % 8 == 0
 // so every 8-feature segment is a 16-byte load.
 template <int DT, int DS2, int PT, bool PAD, bool EXACT>
-__global__ void __launch_bounds__(THREADS, (PT * DS2 <= 16 && DS2 <= 9) ? FKC_AB : 1)
+__global__ void __launch_bounds__(THREADS,
+                                  PT == 8 ? 2
+                                  : (PT * DS2 <= 16 && DS2 <= 9) ? FKC_AB
+                                                                 : 1)
 assign_mfma_kernel(const uint16_t* __restrict__ x,
                    const uint16_t* __restrict__ cent,
                    const float* __restrict__ c_sq, int32_t* __restrict__ ids,
@@ -220,7 +229,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // stays below K).  Only K < KCD clamps rows to K-1.  c_sq lands raw and
     // each wave scales (and masks past K) its own share once its loads are
     // in, before the barrier.
-    constexpr int KCD0 = DS2 <= 4 ? FKC_KC_DMA : 64;
+    constexpr int KCD0 = PT == 8 ? FKC_KC_DMA8 : DS2 <= 4 ? FKC_KC_DMA : 64;
     constexpr int KCD = (KCD0 * DP * 2) % (THREADS * 16) == 0 ? KCD0 : 64;
     constexpr int ROWB = DP * 2;
     constexpr int STAGE = KCD * ROWB;
@@ -321,6 +330,33 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
           u32x4 a[DS2];
           f32x4 ci;
           frag(lc, lq, t, a, ci);
+          f32x4 acc[PT];
+#pragma unroll
+          for (int s = 0; s < DS2; ++s) {
+#pragma unroll
+            for (int p = 0; p < PT; ++p)
+              acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? ci : acc[p]);
+          }
+          fold(acc, kb + 16 * t);
+        }
+      } else if constexpr (PT == 8) {
+        // Eight tiles: the point registers leave no room for a second set
+        // of accumulators, so each block is folded after its own MFMAs; the
+        // next block's fragments are still read a block ahead, and the
+        // compiler overlaps one block's folds with the next block's matrix
+        // work (measured at N=524288, K=8192, D=128: 0.784 -> 0.749 ms
+        // against four tiles, from half the LDS fragment reads and half the
+        // centroid stage traffic per point).
+        u32x4 an[DS2];
+        f32x4 cn;
+        frag(lc, lq, 0, an, cn);
+#pragma unroll
+        for (int t = 0; t < NTD; ++t) {
+          u32x4 a[DS2];
+          f32x4 ci = cn;
+#pragma unroll
+          for (int s = 0; s < DS2; ++s) a[s] = an[s];
+          if (t + 1 < NTD) frag(lc, lq, t + 1, an, cn);
           f32x4 acc[PT];
 #pragma unroll
           for (int s = 0; s < DS2; ++s) {
@@ -582,7 +618,13 @@ using MfmaLauncher = int (*)(const void*, const void*, const float*, int32_t*,
 
 template <int DT, int DS2, int PT>
 constexpr MfmaLauncher entry(bool pad, bool exact) {
-  if constexpr (PT * DS2 * 4 <= 64) {
+  if constexpr (PT == 8) {
+    // Direct stages and the re-score epilogue only (DS2 = 4, unpadded).
+    if constexpr (DS2 == 4) {
+      if (!pad && !exact) return &launch_mfma_t<DT, DS2, PT, false, false>;
+    }
+    return nullptr;
+  } else if constexpr (PT * DS2 * 4 <= 64) {
     if (exact)
       return pad ? &launch_mfma_t<DT, DS2, PT, true, true>
                  : &launch_mfma_t<DT, DS2, PT, false, true>;
@@ -593,14 +635,16 @@ constexpr MfmaLauncher entry(bool pad, bool exact) {
   }
 }
 
-// pt: 16-point tiles per wave (1, 2 or 4).  Variants keep the point
-// registers (PT * DS2 * 4 VGPRs) at <= 64.
+// pt: 16-point tiles per wave (1, 2, 4, or 8 for unpadded D = 128 with the
+// re-score epilogue).  The 1/2/4 variants keep the point registers
+// (PT * DS2 * 4 VGPRs) at <= 64; the eight-tile one holds 128.
 template <int DT, int DS2>
 MfmaLauncher by_pt(int pt, bool pad, bool exact) {
   switch (pt) {
     case 1: return entry<DT, DS2, 1>(pad, exact);
     case 2: return entry<DT, DS2, 2>(pad, exact);
     case 4: return entry<DT, DS2, 4>(pad, exact);
+    case 8: return entry<DT, DS2, 8>(pad, exact);
     default: return nullptr;
   }
 }
@@ -635,16 +679,22 @@ bool assign_uses_mfma(int dtype, int64_t D) {
          D <= 512 && !force_safe_assign();
 }
 
-// Tiles per wave: the largest of 4, 2, 1 (bounded by the 64-VGPR point
-// budget) whose grid still has >= 1024 workgroups (4 per CU on 256 CUs);
-// fewer, fatter workgroups reuse each LDS centroid stage more, but small
-// grids leave CUs idle and hide latency badly (measured at the c2..c5
-// shapes).  FKC_NTILES overrides.
-static int choose_pt(int ds2, int64_t B, int64_t N) {
+// Tiles per wave: the largest of 8 (unpadded D = 128, re-score epilogue
+// only), 4, 2, 1 (bounded by the 64-VGPR point budget) whose grid still has
+// >= 1024 workgroups (4 per CU on 256 CUs); fewer, fatter workgroups reuse
+// each LDS centroid stage more, but small grids leave CUs idle and hide
+// latency badly (measured at the c2..c5 shapes; eight tiles at D = 64 ran
+// slower than four).  FKC_NTILES overrides where the variant exists.
+static bool pt8_ok(int ds2, bool pad, bool exact) {
+  return ds2 == 4 && !pad && !exact;
+}
+
+static int choose_pt(int ds2, bool pad, bool exact, int64_t B, int64_t N) {
   const int o = ntiles_override();
-  if (o != 0 && o * ds2 * 4 <= 64) return o;
-  for (int pt = 4; pt > 1; pt >>= 1) {
-    if (pt * ds2 * 4 > 64) continue;
+  if (o == 8 && pt8_ok(ds2, pad, exact)) return o;
+  if (o != 0 && o != 8 && o * ds2 * 4 <= 64) return o;
+  for (int pt = 8; pt > 1; pt >>= 1) {
+    if (pt == 8 ? !pt8_ok(ds2, pad, exact) : pt * ds2 * 4 > 64) continue;
     const int64_t wgs = B * ((N + 64 * pt - 1) / (64 * pt));
     if (wgs >= 1024) return pt;
   }
@@ -656,11 +706,11 @@ int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                        int64_t D, int dtype, const int32_t* ctrl,
                        hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   const int ds2 = (int)((D + 31) / 32);
-  const int pt = choose_pt(ds2, B, N);
   const bool pad = D != 32 * ds2;
   // Re-scoring the winning block costs about one 16-centroid block per point
   // tile; below this K the exact in-loop index is cheaper.
   const bool exact = K <= FKC_EXACT_MAX_K;
+  const int pt = choose_pt(ds2, pad, exact, B, N);
   MfmaLauncher fn =
       dtype == FKC_F16 ? mfma_launcher<FKC_F16>(ds2, pt, pad, exact)
                        : mfma_launcher<FKC_BF16>(ds2, pt, pad, exact);

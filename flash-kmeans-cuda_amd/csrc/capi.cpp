@@ -46,7 +46,7 @@ int ntiles_override() {
   const char* s = std::getenv("FKC_NTILES");
   if (!s) return 0;
   const int v = std::atoi(s);
-  return (v == 1 || v == 2 || v == 4) ? v : 0;
+  return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
 }
 
 int sort_tile_override() {

@@ -74,12 +74,15 @@ def test_mfma_every_feature_width(dtype, D):
     _check(x, c, dtype, _gpu_assign(x, c, dtype))
 
 
-@pytest.mark.parametrize("ntiles", ["1", "2", "4"])
+@pytest.mark.parametrize("ntiles", ["1", "2", "4", "8"])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_identity_centroids_and_tail(monkeypatch, ntiles, dtype):
-    """First K rows as centroids map to themselves (test_persistent.py:35-64)."""
+    """First K rows as centroids map to themselves (test_persistent.py:35-64).
+    Eight tiles exist only for unpadded D = 128 above the exact-index K; on
+    the other shapes the override falls back to the automatic choice."""
     monkeypatch.setenv("FKC_NTILES", ntiles)
-    for (N, K, D) in [(4096, 64, 128), (257, 16, 128), (8192, 128, 64)]:
+    for (N, K, D) in [(4096, 64, 128), (257, 16, 128), (8192, 128, 64),
+                      (3000, 600, 128)]:
         x, _ = _data(1, N, 1, D, dtype, seed=N)
         c = x[:, :K].copy()
         got = _gpu_assign(x, c, dtype)
@@ -124,6 +127,22 @@ def test_determinism_and_ntiles_invariance(monkeypatch, dtype):
         outs.append(_gpu_assign(x, c, dtype))
     for o in outs[1:]:
         assert np.array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("B,N,K", [(1, 5000, 520), (2, 3001, 1000), (1, 700, 4097)])
+def test_eight_tiles_match_oracle_and_four(monkeypatch, dtype, B, N, K):
+    """The eight-tile variant (128 points per wave, 128-row stages; D = 128,
+    K above the exact-index cutoff) against the oracle and, bit for bit,
+    against four tiles: ragged N (partial workgroups), K not a multiple of
+    the 128-row stage (the last stage re-scores rows), batches."""
+    x, c = _data(B, N, K, 128, dtype, seed=N + K)
+    monkeypatch.setenv("FKC_NTILES", "8")
+    got8 = _gpu_assign(x, c, dtype)
+    monkeypatch.setenv("FKC_NTILES", "4")
+    got4 = _gpu_assign(x, c, dtype)
+    assert np.array_equal(got8, got4)
+    _check(x, c, dtype, got8, max_frac=1e-3)
 
 
 @pytest.mark.parametrize("B,N,K,D", [(1, 4096, 64, 128), (2, 1000, 33, 37), (1, 513, 300, 16)])
