@@ -62,7 +62,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
 // FKC_KC_DMA, centroid rows per direct stage (D <= 128); FKC_KC_DMA8, the
 // same for the eight-tile variant (two workgroups per CU leave it twice the
-// LDS); FKC_SCHED_GROUPS,
+// LDS); FKC_SLICE_MIN_ROWS, the shortest centroid slice; FKC_SCHED_GROUPS,
 // LDS-read / MFMA / VALU ordering hints in the direct-stage loop.
 #ifndef FKC_AB
 #define FKC_AB 2
@@ -78,6 +78,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #endif
 #ifndef FKC_KC_DMA8
 #define FKC_KC_DMA8 128
+#endif
+#ifndef FKC_SLICE_MIN_ROWS
+#define FKC_SLICE_MIN_ROWS 2048
 #endif
 #ifndef FKC_SCHED_GROUPS
 #define FKC_SCHED_GROUPS 1
@@ -149,8 +152,19 @@ __global__ void __launch_bounds__(THREADS,
 assign_mfma_kernel(const uint16_t* __restrict__ x,
                    const uint16_t* __restrict__ cent,
                    const float* __restrict__ c_sq, int32_t* __restrict__ ids,
-                   int N, int K, int D, const int32_t* __restrict__ ctrl) {
+                   int N, int K, int D, const int32_t* __restrict__ ctrl,
+                   int kspan, float* __restrict__ psc,
+                   int32_t* __restrict__ pidx) {
   if (loop_done(ctrl)) return;
+  // Centroid slice (grid z): rows k0 .. k0 + kspan - 1 of the batch's K,
+  // scored below as a problem of K' = min(K - k0, kspan) rows.  With one
+  // slice the winner goes to ids; with several, each slice writes its
+  // winner's score and row to psc / pidx and assign_merge_kernel picks the
+  // first maximum in slice order (the slices' scores are the same MFMA
+  // chains as unsliced, so the labels are identical).
+  const int Kall = K;
+  const int k0 = blockIdx.z * kspan;
+  K = min(Kall - k0, kspan);
   constexpr int DP = DS2 * 32;
   constexpr int ROW = DP + 8;       // LDS row stride in 16-bit elements
   constexpr int SEGS = DP / 8;      // 16-byte segments per padded row
@@ -172,8 +186,8 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
   const int dsegs = D / 8;          // real segments per row
   constexpr bool padded = PAD;
   const uint16_t* xb = x + (size_t)b * N * D;
-  const uint16_t* cb = cent + (size_t)b * K * D;
-  const float* qb = c_sq + (size_t)b * K;
+  const uint16_t* cb = cent + ((size_t)b * Kall + k0) * D;
+  const float* qb = c_sq + (size_t)b * Kall + k0;
   const int n0 = blockIdx.x * PTS_WG + wave * PTS_WAVE;
 
   // B operand: point n0+16p+col, features 32s + 8g .. +7.  Points past N
@@ -528,7 +542,15 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
         }
       }
       const int n = n0 + 16 * p + col;
-      if (g == 0 && n < N) ids[(size_t)b * N + n] = bi;
+      if (g == 0 && n < N) {
+        if (psc != nullptr) {
+          const size_t o = ((size_t)b * gridDim.z + blockIdx.z) * N + n;
+          psc[o] = bv;
+          pidx[o] = k0 + bi;
+        } else {
+          ids[(size_t)b * N + n] = bi;
+        }
+      }
     }
     return;
   }
@@ -584,37 +606,91 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       }
     }
     const int n = n0 + 16 * p + col;
-    if (g == (col >> 2) && n < N) ids[(size_t)b * N + n] = base + rr;
+    if (g == (col >> 2) && n < N) {
+      if (psc != nullptr) {
+        const size_t o = ((size_t)b * gridDim.z + blockIdx.z) * N + n;
+        psc[o] = m;
+        pidx[o] = k0 + base + rr;
+      } else {
+        ids[(size_t)b * N + n] = base + rr;
+      }
+    }
   }
 }
 
-// ev0 / ev1 (both null or both set): events that the dispatch packet itself
-// stamps at the kernel's start and end (no marker packets in the stream).
+// Merge of centroid slices: per point, the first slice (lowest rows) with
+// the maximal score wins, and within a slice the kernel already kept the
+// first maximal row, so the label is the lowest index of the maximum, as
+// unsliced.
+__global__ void __launch_bounds__(256)
+assign_merge_kernel(const float* __restrict__ psc,
+                    const int32_t* __restrict__ pidx, int32_t* __restrict__ ids,
+                    int N, int S, const int32_t* __restrict__ ctrl) {
+  if (loop_done(ctrl)) return;
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const size_t b = blockIdx.y;
+  const size_t o = b * S * N + n;
+  float best = psc[o];
+  int bi = pidx[o];
+  for (int z = 1; z < S; ++z) {
+    const float v = psc[o + (size_t)z * N];
+    const int i = pidx[o + (size_t)z * N];
+    bi = v > best ? i : bi;
+    best = fmaxf(best, v);
+  }
+  ids[b * N + n] = bi;
+}
+
+// Centroid slicing of one launch: S slices of kspan rows (S = 1: none);
+// psc / pidx hold B x S x N partial winners when S > 1.
+struct Slices {
+  int S = 1;
+  int kspan = 0;
+  float* psc = nullptr;
+  int32_t* pidx = nullptr;
+};
+
+// ev0 / ev1 (both null or both set): events that the dispatch packets
+// themselves stamp, ev0 at the start of the scoring kernel and ev1 at the
+// end of the last kernel (no marker packets in the stream).
 template <int DT, int DS2, int PT, bool PAD, bool EXACT>
 int launch_mfma_t(const void* x, const void* c, const float* c_sq,
                   int32_t* ids, int64_t B, int64_t N, int64_t K, int64_t D,
-                  const int32_t* ctrl, hipStream_t s, hipEvent_t ev0,
-                  hipEvent_t ev1) {
+                  const int32_t* ctrl, const Slices& sl, hipStream_t s,
+                  hipEvent_t ev0, hipEvent_t ev1) {
   constexpr int PTS_WG = 4 * PT * 16;
-  dim3 grid((unsigned)((N + PTS_WG - 1) / PTS_WG), (unsigned)B);
+  const bool merge = sl.S > 1;
+  dim3 grid((unsigned)((N + PTS_WG - 1) / PTS_WG), (unsigned)B,
+            (unsigned)sl.S);
+  const int kspan = merge ? sl.kspan : (int)K;
   if (ev0 != nullptr)
     hipExtLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
-                          dim3(THREADS), 0, s, ev0, ev1, 0,
+                          dim3(THREADS), 0, s, ev0, merge ? nullptr : ev1, 0,
                           static_cast<const uint16_t*>(x),
                           static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
-                          (int)K, (int)D, ctrl);
+                          (int)K, (int)D, ctrl, kspan, sl.psc, sl.pidx);
   else
     hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
                        dim3(THREADS), 0, s, static_cast<const uint16_t*>(x),
                        static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
-                       (int)K, (int)D, ctrl);
-  return check_launch("assign_mfma");
+                       (int)K, (int)D, ctrl, kspan, sl.psc, sl.pidx);
+  if (int rc = check_launch("assign_mfma")) return rc;
+  if (!merge) return FKC_OK;
+  dim3 mgrid((unsigned)((N + 255) / 256), (unsigned)B);
+  if (ev1 != nullptr)
+    hipExtLaunchKernelGGL(assign_merge_kernel, mgrid, dim3(256), 0, s, nullptr,
+                          ev1, 0, sl.psc, sl.pidx, ids, (int)N, sl.S, ctrl);
+  else
+    hipLaunchKernelGGL(assign_merge_kernel, mgrid, dim3(256), 0, s, sl.psc,
+                       sl.pidx, ids, (int)N, sl.S, ctrl);
+  return check_launch("assign_merge");
 }
 
 using MfmaLauncher = int (*)(const void*, const void*, const float*, int32_t*,
                              int64_t, int64_t, int64_t, int64_t,
-                             const int32_t*, hipStream_t, hipEvent_t,
-                             hipEvent_t);
+                             const int32_t*, const Slices&, hipStream_t,
+                             hipEvent_t, hipEvent_t);
 
 template <int DT, int DS2, int PT>
 constexpr MfmaLauncher entry(bool pad, bool exact) {
@@ -679,45 +755,134 @@ bool assign_uses_mfma(int dtype, int64_t D) {
          D <= 512 && !force_safe_assign();
 }
 
-// Tiles per wave: the largest of 8 (unpadded D = 128, re-score epilogue
-// only), 4, 2, 1 (bounded by the 64-VGPR point budget) whose grid still has
-// >= 1024 workgroups (4 per CU on 256 CUs); fewer, fatter workgroups reuse
-// each LDS centroid stage more, but small grids leave CUs idle and hide
-// latency badly (measured at the c2..c5 shapes; eight tiles at D = 64 ran
-// slower than four).  FKC_NTILES overrides where the variant exists.
+// Workgroups an unsliced launch of pt tiles needs to fill the chip: 1024
+// (4 per CU) in general; 256 (one per CU, one wave per SIMD) suffice for
+// four tiles at D = 97..128, whose 16 MFMAs per centroid block keep a lone
+// wave busy (measured at N = 131072, K = 2048 and N = 65536, K = 8192:
+// four tiles on 512 / 256 workgroups beat two tiles on 1024 / 512 by 3% /
+// 5%); eight tiles run 2 workgroups per CU and need two rounds of them.
+static int64_t fill_wgs(int pt, int ds2, bool exact) {
+  return (!exact && pt == 4 && ds2 == 4) ? 256 : 1024;
+}
+
+static int64_t grid_wgs(int pt, int64_t B, int64_t N) {
+  return B * ((N + 64 * pt - 1) / (64 * pt));
+}
+
 static bool pt8_ok(int ds2, bool pad, bool exact) {
   return ds2 == 4 && !pad && !exact;
 }
 
+// Tiles per wave for an unsliced launch: the largest of 8 (unpadded
+// D = 128, re-score epilogue only), 4, 2, 1 (bounded by the 64-VGPR point
+// budget) whose grid fills the chip (fill_wgs); fewer, fatter workgroups
+// reuse each LDS centroid stage more, but grids that leave CUs idle hide
+// latency badly (measured at the c2..c5 shapes; eight tiles at D = 64 ran
+// slower than four).  FKC_NTILES overrides where the variant exists.
 static int choose_pt(int ds2, bool pad, bool exact, int64_t B, int64_t N) {
   const int o = ntiles_override();
   if (o == 8 && pt8_ok(ds2, pad, exact)) return o;
   if (o != 0 && o != 8 && o * ds2 * 4 <= 64) return o;
   for (int pt = 8; pt > 1; pt >>= 1) {
     if (pt == 8 ? !pt8_ok(ds2, pad, exact) : pt * ds2 * 4 > 64) continue;
-    const int64_t wgs = B * ((N + 64 * pt - 1) / (64 * pt));
-    if (wgs >= 1024) return pt;
+    if (grid_wgs(pt, B, N) >= fill_wgs(pt, ds2, exact)) return pt;
   }
   return 1;
+}
+
+struct Plan {
+  int ds2, pt, S, kspan;
+  bool pad, exact;
+};
+
+// Launch plan.  K is sliced only when no unsliced grid fills the chip (few
+// points, many centroids): the most tiles the point budget allows (four up
+// to D = 128) then run on S slices of kspan rows
+// (a multiple of 128, at least FKC_SLICE_MIN_ROWS) scored by separate
+// workgroups, and a small kernel merges them.  Each slice re-reads its
+// points and ends with its own re-score, so short slices lose: at
+// N = 131072, K = 2048, D = 128 four slices of 512 rows took 0.124 ms
+// against 0.073 ms unsliced; at N = 80000, K = 70000, D = 16 four slices
+// took 0.376 ms against 0.756 ms, and at N = 8192, K = 65536, D = 128
+// eight slices 0.150 ms against 0.531 ms.  FKC_KSPLIT forces S.
+static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
+                        bool can_slice) {
+  Plan p;
+  p.ds2 = (int)((D + 31) / 32);
+  p.pad = D != 32 * p.ds2;
+  // Re-scoring the winning block costs about one 16-centroid block per point
+  // tile; below this K the exact in-loop index is cheaper.
+  p.exact = K <= FKC_EXACT_MAX_K;
+  p.pt = choose_pt(p.ds2, p.pad, p.exact, B, N);
+  p.S = 1;
+  p.kspan = (int)K;
+  if (!can_slice || p.exact) return p;
+  // Four tiles, not eight: on sliced-size grids four tiles on ~256
+  // workgroups beat eight on 512 (N = 8192, K = 65536: 0.150 vs 0.166 ms;
+  // N = 16384, K = 32768: 0.142 vs 0.156 ms).
+  int pt = p.pt;
+  if (ntiles_override() == 0) pt = p.ds2 <= 4 ? 4 : p.ds2 <= 8 ? 2 : 1;
+  const int64_t tiles = grid_wgs(pt, B, N);
+  const int64_t want = fill_wgs(pt, p.ds2, p.exact);
+  int64_t S = ksplit_override();
+  if (S == 0) {
+    if (tiles >= want) return p;
+    S = 1;
+    while (tiles * S < want && K / (2 * S) >= FKC_SLICE_MIN_ROWS) S *= 2;
+    // Slices that still leave the chip short only pay off when the unsliced
+    // grid is short too.
+    if (tiles * S < want &&
+        grid_wgs(p.pt, B, N) >= fill_wgs(p.pt, p.ds2, p.exact))
+      return p;
+  }
+  const int64_t span = ((K + S - 1) / S + 127) / 128 * 128;
+  S = (K + span - 1) / span;
+  if (S <= 1) return p;
+  p.pt = pt;
+  p.S = (int)S;
+  p.kspan = (int)span;
+  return p;
+}
+
+static size_t slice_bytes(const Plan& p, int64_t B, int64_t N, Slices* sl,
+                          void* ws) {
+  if (p.S <= 1) return 0;
+  Carve c(ws);
+  float* psc = c.take<float>((size_t)B * p.S * N);
+  int32_t* pidx = c.take<int32_t>((size_t)B * p.S * N);
+  if (sl) {
+    sl->S = p.S;
+    sl->kspan = p.kspan;
+    sl->psc = psc;
+    sl->pidx = pidx;
+  }
+  return c.used;
+}
+
+size_t assign_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,
+                              int dtype) {
+  if (!assign_uses_mfma(dtype, D) || B * N == 0 || K < 1) return 0;
+  return slice_bytes(plan_assign(B, N, K, D, true), B, N, nullptr, nullptr);
 }
 
 int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                        int32_t* ids, int64_t B, int64_t N, int64_t K,
                        int64_t D, int dtype, const int32_t* ctrl,
-                       hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
-  const int ds2 = (int)((D + 31) / 32);
-  const bool pad = D != 32 * ds2;
-  // Re-scoring the winning block costs about one 16-centroid block per point
-  // tile; below this K the exact in-loop index is cheaper.
-  const bool exact = K <= FKC_EXACT_MAX_K;
-  const int pt = choose_pt(ds2, pad, exact, B, N);
+                       hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
+                       void* ws, size_t ws_bytes) {
+  const Plan p = plan_assign(B, N, K, D, ws != nullptr);
+  Slices sl;
+  const size_t need = slice_bytes(p, B, N, &sl, ws);
+  if (need > ws_bytes)
+    return fail(FKC_ERR_WORKSPACE, "assign: workspace %zu < %zu bytes",
+                ws_bytes, need);
   MfmaLauncher fn =
-      dtype == FKC_F16 ? mfma_launcher<FKC_F16>(ds2, pt, pad, exact)
-                       : mfma_launcher<FKC_BF16>(ds2, pt, pad, exact);
+      dtype == FKC_F16 ? mfma_launcher<FKC_F16>(p.ds2, p.pt, p.pad, p.exact)
+                       : mfma_launcher<FKC_BF16>(p.ds2, p.pt, p.pad, p.exact);
   if (!fn)
     return fail(FKC_ERR_UNSUPPORTED, "assign: no MFMA variant for D=%lld",
                 (long long)D);
-  return fn(x, c, c_sq, ids, B, N, K, D, ctrl, s, ev0, ev1);
+  return fn(x, c, c_sq, ids, B, N, K, D, ctrl, sl, s, ev0, ev1);
 }
 
 }  // namespace fkc

@@ -26,7 +26,8 @@ namespace fkc {
 int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                        int32_t* ids, int64_t B, int64_t N, int64_t K,
                        int64_t D, int dtype, const int32_t* ctrl,
-                       hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+                       hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
+                       void* ws, size_t ws_bytes);
 
 namespace {
 
@@ -202,11 +203,12 @@ int launch_rowsq_t(const void* src, float* out, int64_t rows, int64_t D,
 int launch_assign(const void* x, const void* c, const float* x_sq,
                   const float* c_sq, int32_t* ids, int64_t B, int64_t N,
                   int64_t K, int64_t D, int dtype, const int32_t* ctrl,
-                  hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+                  hipStream_t s, hipEvent_t ev0, hipEvent_t ev1, void* ws,
+                  size_t ws_bytes) {
   if (B == 0 || N == 0) return FKC_OK;
   if (assign_uses_mfma(dtype, D))
     return launch_assign_mfma(x, c, c_sq, ids, B, N, K, D, dtype, ctrl, s,
-                              ev0, ev1);
+                              ev0, ev1, ws, ws_bytes);
   // The VALU route marks its span with event records on the stream.
   if (ev0 != nullptr) (void)hipEventRecord(ev0, s);
   int rc = FKC_OK;

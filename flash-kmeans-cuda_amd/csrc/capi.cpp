@@ -49,6 +49,13 @@ int ntiles_override() {
   return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
 }
 
+int ksplit_override() {
+  const char* s = std::getenv("FKC_KSPLIT");
+  if (!s) return 0;
+  const int v = std::atoi(s);
+  return (v >= 1 && v <= 64) ? v : 0;
+}
+
 int sort_tile_override() {
   const char* s = std::getenv("FKC_SORT_TILE");
   if (!s) return 0;
@@ -109,6 +116,8 @@ struct LoopBuffers {
   size_t sort_ws_bytes = 0;
   void* upd_ws = nullptr;
   size_t upd_ws_bytes = 0;
+  void* asg_ws = nullptr;  // sliced assign's partial winners (may be empty)
+  size_t asg_ws_bytes = 0;
 };
 
 LoopBuffers carve_loop(void* ws, int64_t B, int64_t N, int64_t K, int64_t D,
@@ -127,6 +136,8 @@ LoopBuffers carve_loop(void* ws, int64_t B, int64_t N, int64_t K, int64_t D,
   L.sort_ws = c.take<char>(L.sort_ws_bytes);
   L.upd_ws_bytes = update_workspace_bytes(B, N, D);
   L.upd_ws = c.take<char>(L.upd_ws_bytes);
+  L.asg_ws_bytes = assign_workspace_bytes(B, N, K, D, dtype);
+  L.asg_ws = L.asg_ws_bytes ? c.take<char>(L.asg_ws_bytes) : nullptr;
   if (total) *total = c.used;
   return L;
 }
@@ -152,6 +163,41 @@ int fkc_euclid_assign(const void* x, const void* centroids, const float* x_sq,
     return fail(FKC_ERR_INVALID, "euclid_assign: null pointer argument");
   return launch_assign(x, centroids, x_sq, c_sq, cluster_ids, B, N, K, D, dtype,
                        nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t fkc_euclid_assign_workspace_bytes(int64_t B, int64_t N, int64_t K,
+                                         int64_t D, int dtype) {
+  if (shape_ok(B, N, K, D, "euclid_assign_workspace_bytes") ||
+      dtype_ok(dtype, "euclid_assign_workspace_bytes"))
+    return 0;
+  return assign_workspace_bytes(B, N, K, D, dtype);
+}
+
+int fkc_euclid_assign_ws(const void* x, const void* centroids,
+                         const float* x_sq, const float* c_sq,
+                         int32_t* cluster_ids, int64_t B, int64_t N, int64_t K,
+                         int64_t D, int dtype, void* workspace,
+                         size_t workspace_bytes, fkc_stream_t stream) {
+  g_err[0] = 0;
+  if (int rc = shape_ok(B, N, K, D, "euclid_assign_ws")) return rc;
+  if (int rc = dtype_ok(dtype, "euclid_assign_ws")) return rc;
+  if (B * N == 0) return FKC_OK;
+  if (!x || !centroids || !c_sq || !cluster_ids)
+    return fail(FKC_ERR_INVALID, "euclid_assign_ws: null pointer argument");
+  const size_t need = assign_workspace_bytes(B, N, K, D, dtype);
+  if (need == 0)
+    return launch_assign(x, centroids, x_sq, c_sq, cluster_ids, B, N, K, D,
+                         dtype, nullptr, reinterpret_cast<hipStream_t>(stream));
+  if (!workspace || workspace_bytes < need)
+    return fail(FKC_ERR_WORKSPACE, "euclid_assign_ws: workspace %zu < %zu bytes",
+                workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) % kWorkspaceAlign != 0)
+    return fail(FKC_ERR_WORKSPACE,
+                "euclid_assign_ws: workspace not %d-byte aligned",
+                kWorkspaceAlign);
+  return launch_assign(x, centroids, x_sq, c_sq, cluster_ids, B, N, K, D, dtype,
+                       nullptr, reinterpret_cast<hipStream_t>(stream), nullptr,
+                       nullptr, workspace, workspace_bytes);
 }
 
 int fkc_row_sqnorm(const void* src, float* out, int64_t rows, int64_t D,
@@ -332,7 +378,7 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
       g_prof.stops.push_back(e1);
     }
     rc = launch_assign(x, centroids, L.x_sq, L.c_sq, cluster_ids, B, N, K, D,
-                       dtype, ctrl, s, e0, e1);
+                       dtype, ctrl, s, e0, e1, L.asg_ws, L.asg_ws_bytes);
     if (!rc)
       rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
                              L.sort_ws, L.sort_ws_bytes, ctrl, s, it & 1);

@@ -40,13 +40,20 @@ struct Carve {
 // ---------------------------------------------------------------- assign
 // Routing predicate: the MFMA kernel serves fp16/bf16, D % 8 == 0, D <= 512.
 bool assign_uses_mfma(int dtype, int64_t D);
+// Workspace bytes of a sliced MFMA assign (centroid slices scored by
+// separate workgroups, then merged) for this shape; 0 when it is not sliced.
+size_t assign_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,
+                              int dtype);
 // ev0 / ev1 (optional, both or neither): timing events of the launch; on
-// the MFMA route the dispatch packet stamps them (no extra stream packets).
+// the MFMA route the dispatch packets stamp them (no extra stream packets).
+// ws (optional, assign_workspace_bytes): with it the MFMA route may slice K;
+// without it the launch is never sliced.
 int launch_assign(const void* x, const void* c, const float* x_sq,
                   const float* c_sq, int32_t* ids, int64_t B, int64_t N,
                   int64_t K, int64_t D, int dtype, const int32_t* ctrl,
                   hipStream_t s, hipEvent_t ev0 = nullptr,
-                  hipEvent_t ev1 = nullptr);
+                  hipEvent_t ev1 = nullptr, void* ws = nullptr,
+                  size_t ws_bytes = 0);
 int launch_row_sqnorm(const void* src, float* out, int64_t rows, int64_t D,
                       int dtype, const int32_t* ctrl, hipStream_t s);
 
@@ -122,7 +129,9 @@ int launch_quality(const void* x, const void* c, const int32_t* ids,
                    double* inertia, int32_t* empty, void* ws, size_t ws_bytes,
                    hipStream_t s);
 
-// FKC_NTILES=1|2|4: 16-point tiles per wave in the MFMA kernel; 0 = auto.
+// FKC_NTILES=1|2|4|8: 16-point tiles per wave in the MFMA kernel; 0 = auto.
 int ntiles_override();
+// FKC_KSPLIT=1..64: centroid slices of a sliced MFMA assign; 0 = auto.
+int ksplit_override();
 
 }  // namespace fkc

@@ -61,10 +61,22 @@ def euclid_assign(x: torch.Tensor, centroids: torch.Tensor, x_sq: torch.Tensor,
     if x_sq is not None and x_sq.numel() == B * N:
         _contig(x_sq)
         xsq_ptr = x_sq.data_ptr()
-    _lib.check(_lib.lib.fkc_euclid_assign(
-        x.data_ptr(), centroids.data_ptr(), xsq_ptr, c_sq.data_ptr(),
-        out.data_ptr(), B, N, K, D, _lib.dtype_code(x.dtype), _lib.stream_of(x)),
-        "euclid_assign")
+    dt = _lib.dtype_code(x.dtype)
+    need = _lib.lib.fkc_euclid_assign_workspace_bytes(B, N, K, D, dt)
+    if need == 0:
+        _lib.check(_lib.lib.fkc_euclid_assign(
+            x.data_ptr(), centroids.data_ptr(), xsq_ptr, c_sq.data_ptr(),
+            out.data_ptr(), B, N, K, D, dt, _lib.stream_of(x)),
+            "euclid_assign")
+    else:
+        # Shapes whose point tiles alone cannot fill the GPU slice K across
+        # workgroups; the partial winners live in a stream-ordered workspace.
+        ws = _lib.workspace(need, x.device)
+        _lib.check(_lib.lib.fkc_euclid_assign_ws(
+            x.data_ptr(), centroids.data_ptr(), xsq_ptr, c_sq.data_ptr(),
+            out.data_ptr(), B, N, K, D, dt, ws.data_ptr(), ws.numel(),
+            _lib.stream_of(x)),
+            "euclid_assign")
     return out
 
 

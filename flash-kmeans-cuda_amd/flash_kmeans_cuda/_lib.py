@@ -28,6 +28,8 @@ SIGNATURES = {
     "fkc_last_error": (ctypes.c_char_p, []),
     "fkc_version": (ctypes.c_char_p, []),
     "fkc_euclid_assign": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
+    "fkc_euclid_assign_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _int]),
+    "fkc_euclid_assign_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
     "fkc_row_sqnorm": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
     "fkc_label_sort_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "fkc_label_sort": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),

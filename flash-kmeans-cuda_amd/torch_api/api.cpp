@@ -122,10 +122,20 @@ at::Tensor euclid_assign_out(const at::Tensor& x, const at::Tensor& centroids,
     TORCH_CHECK(x_sq.is_contiguous(), "all tensors must be contiguous");
     xsq = x_sq.data_ptr<float>();
   }
-  check_rc(fkc_euclid_assign(x.data_ptr(), centroids.data_ptr(), xsq, c_sq.data_ptr<float>(),
-                             cluster_ids.data_ptr<int32_t>(), B, N, K, D, dtype_code(x),
-                             stream_of(x)),
-           "euclid_assign");
+  const size_t need = fkc_euclid_assign_workspace_bytes(B, N, K, D, dtype_code(x));
+  if (need == 0) {
+    check_rc(fkc_euclid_assign(x.data_ptr(), centroids.data_ptr(), xsq, c_sq.data_ptr<float>(),
+                               cluster_ids.data_ptr<int32_t>(), B, N, K, D, dtype_code(x),
+                               stream_of(x)),
+             "euclid_assign");
+  } else {
+    // K sliced across workgroups: partial winners in a stream-ordered workspace.
+    at::Tensor ws = workspace(need, x);
+    check_rc(fkc_euclid_assign_ws(x.data_ptr(), centroids.data_ptr(), xsq,
+                                  c_sq.data_ptr<float>(), cluster_ids.data_ptr<int32_t>(), B, N,
+                                  K, D, dtype_code(x), ws.data_ptr(), ws.numel(), stream_of(x)),
+             "euclid_assign");
+  }
   return cluster_ids;
 }
 

@@ -78,6 +78,30 @@ FKC_CAPI int fkc_euclid_assign(const void* x, const void* centroids,
                                int64_t K, int64_t D, int dtype,
                                fkc_stream_t stream);
 
+/*
+ * Workspace variant of fkc_euclid_assign, same labels.  When the point
+ * tiles of a shape cannot fill the GPU (fewer than ~1024 workgroups: N of
+ * a few 100K or less with K > 512 at D = 128), the MFMA route cuts K into
+ * slices scored by separate workgroups and merges their winners (first
+ * maximum in slice order, so the lowest index still wins exact ties); the
+ * workspace holds the partial winners, 8 bytes per point and slice.
+ * fkc_euclid_assign_workspace_bytes returns the bytes needed (0: the shape
+ * is not sliced and the workspace may be NULL); the workspace is 256-byte
+ * aligned and may be reused once the call's stream work is done.  Same
+ * reference interfaces as fkc_euclid_assign (flash_kmeans_cuda.h:41-46,
+ * bindings.cpp:43-63); the slicing has no counterpart there (the reference
+ * picks among tile shapes per dtype, D and K, assign_sm80.cu:707-1111).
+ */
+FKC_CAPI size_t fkc_euclid_assign_workspace_bytes(int64_t B, int64_t N,
+                                                  int64_t K, int64_t D,
+                                                  int dtype);
+FKC_CAPI int fkc_euclid_assign_ws(const void* x, const void* centroids,
+                                  const float* x_sq, const float* c_sq,
+                                  int32_t* cluster_ids, int64_t B, int64_t N,
+                                  int64_t K, int64_t D, int dtype,
+                                  void* workspace, size_t workspace_bytes,
+                                  fkc_stream_t stream);
+
 /* out[r] = sum_d float(src[r,d])^2 for r < rows.  Replaces the torch
  * expressions (c.float()**2).sum(-1) at kmeans.py:94 and x.float()**2 at
  * kmeans.py:151. */

@@ -110,17 +110,68 @@ def test_invalid_arguments_are_rejected_without_a_device():
     assert rc == 2 and "aligned" in msg
     assert L.fkc_assigned_inertia(fake, fake, fake, 1, 10, 4, 8, 1, None, None,
                                   None, 0, None) == 0  # nothing asked
+    # sliced assign: a shape that slices K (N = 5000, K = 4096, D = 128 fp16)
+    # needs its workspace; short, missing and misaligned ones are refused
+    need = L.fkc_euclid_assign_workspace_bytes(1, 5000, 4096, 128, 1)
+    assert need > 0
+    rc, msg = _err(L.fkc_euclid_assign_ws(fake, fake, None, fake, fake, 1, 5000, 4096, 128, 1,
+                                          fake, need - 1, None))
+    assert rc == 2 and "workspace" in msg
+    rc, msg = _err(L.fkc_euclid_assign_ws(fake, fake, None, fake, fake, 1, 5000, 4096, 128, 1,
+                                          None, 0, None))
+    assert rc == 2 and "workspace" in msg
+    rc, msg = _err(L.fkc_euclid_assign_ws(fake, fake, None, fake, fake, 1, 5000, 4096, 128, 1,
+                                          odd, need, None))
+    assert rc == 2 and "aligned" in msg
+    rc, msg = _err(L.fkc_euclid_assign_ws(None, fake, None, fake, fake, 1, 5000, 4096, 128, 1,
+                                          fake, need, None))
+    assert rc == 1 and "null" in msg
+    rc, msg = _err(L.fkc_euclid_assign_ws(fake, fake, None, fake, fake, 1, 10, 4, 16, 7,
+                                          None, 0, None))
+    assert rc == 1 and "dtype" in msg
 
 
 def test_empty_inputs_are_no_ops():
     from flash_kmeans_cuda import _lib
     L = _lib.lib
     assert L.fkc_euclid_assign(None, None, None, None, None, 0, 0, 4, 16, 1, None) == 0
+    assert L.fkc_euclid_assign_ws(None, None, None, None, None, 0, 0, 4, 16, 1, None, 0,
+                                  None) == 0
     assert L.fkc_label_sort(None, None, None, 1, 0, 4, None, 0, None) == 0
     n = ctypes.c_int32(-1)
     assert L.fkc_kmeans_lloyd(None, None, None, 1, 100, 4, 8, 1, 0, 0.0, None, 0, None,
                               None, ctypes.byref(n)) == 0
     assert n.value == 0
+
+
+def test_assign_slice_plan(monkeypatch):
+    """Which shapes slice K and how large the partial-winner workspace is
+    (8 bytes per point and slice, each half 256-byte aligned).  None where an
+    unsliced grid fills the chip: the benchmark shape (c5, 1024 eight-tile
+    workgroups), c3 and c5's one-GPU share of eight (four tiles on 512 / 256
+    workgroups), c4 (2048 four-tile workgroups); none for K <= 512 (exact
+    in-loop index), the fp32 route, or slices shorter than 2048 rows.
+    FKC_KSPLIT forces a count."""
+    from flash_kmeans_cuda import _lib
+    monkeypatch.delenv("FKC_KSPLIT", raising=False)
+    monkeypatch.delenv("FKC_NTILES", raising=False)
+    f = _lib.lib.fkc_euclid_assign_workspace_bytes
+    half = lambda n: (n * 4 + 255) // 256 * 256
+    assert f(1, 524288, 8192, 128, 1) == 0
+    assert f(1, 131072, 2048, 128, 1) == 0
+    assert f(1, 65536, 8192, 128, 2) == 0
+    assert f(1, 32768, 256, 128, 1) == 0
+    assert f(8, 65536, 1024, 64, 2) == 0
+    assert f(1, 131072, 2048, 128, 0) == 0
+    assert f(2, 30000, 2000, 32, 2) == 0                   # slices would be < 2048 rows
+    assert f(1, 80000, 70000, 16, 1) == 2 * half(4 * 80000)
+    assert f(1, 700, 4097, 128, 1) == 2 * half(2 * 700)    # 2176-row slices
+    assert f(1, 700, 9000, 128, 1) == 2 * half(4 * 700)    # 2304-row slices
+    assert f(1, 10, 4, 16, 7) == 0                         # invalid dtype
+    monkeypatch.setenv("FKC_KSPLIT", "8")
+    assert f(1, 3000, 1030, 128, 2) == 2 * half(5 * 3000)  # 256-row slices
+    monkeypatch.setenv("FKC_KSPLIT", "1")
+    assert f(1, 80000, 70000, 16, 1) == 0
 
 
 def test_workspace_sizes():

@@ -145,6 +145,66 @@ def test_eight_tiles_match_oracle_and_four(monkeypatch, dtype, B, N, K):
     _check(x, c, dtype, got8, max_frac=1e-3)
 
 
+SLICE_CASES = [
+    # (B, N, K, D, dtype, FKC_KSPLIT or None for the automatic plan)
+    (1, 5000, 4096, 128, "f16", None),     # 2 slices of 2048 rows
+    (2, 3001, 4500, 128, "bf16", None),    # 2 slices, ragged N, batches
+    (1, 700, 9000, 128, "f16", None),      # 4 slices, last one 2088 rows
+    (1, 3000, 1030, 128, "bf16", "8"),     # 5 slices, last one 6 rows
+    (1, 2000, 700, 128, "f16", "3"),       # 3 slices of 256 / 256 / 188
+    (2, 4000, 5000, 32, "bf16", None),     # 4 point tiles, 2 slices
+    (1, 3000, 1500, 72, "f16", "2"),       # padded width (register stages)
+]
+
+
+@pytest.mark.parametrize("B,N,K,D,dtype,ksplit", SLICE_CASES)
+def test_sliced_assign_matches_unsliced(monkeypatch, B, N, K, D, dtype, ksplit):
+    """K cut into slices scored by separate workgroups and merged: labels
+    bit-identical to the unsliced launch (same MFMA chain per score, first
+    maximum in slice order) and within the oracle's near-tie bar."""
+    from flash_kmeans_cuda import _lib
+    x, c = _data(B, N, K, D, dtype, seed=N + K + D)
+    if ksplit is None:
+        monkeypatch.delenv("FKC_KSPLIT", raising=False)
+    else:
+        monkeypatch.setenv("FKC_KSPLIT", ksplit)
+    dt = {"f16": 1, "bf16": 2}[dtype]
+    assert _lib.lib.fkc_euclid_assign_workspace_bytes(B, N, K, D, dt) > 0
+    got = _gpu_assign(x, c, dtype)
+    monkeypatch.setenv("FKC_KSPLIT", "1")
+    assert _lib.lib.fkc_euclid_assign_workspace_bytes(B, N, K, D, dt) == 0
+    ref = _gpu_assign(x, c, dtype)
+    assert np.array_equal(got, ref)
+    _check(x, c, dtype, got, max_frac=1e-3)
+
+
+def test_sliced_assign_workspace_errors(monkeypatch):
+    """fkc_euclid_assign_ws rejects a short or misaligned workspace with
+    FKC_ERR_WORKSPACE before launching anything, and needs none when the
+    shape is not sliced."""
+    from flash_kmeans_cuda import _lib
+    monkeypatch.delenv("FKC_KSPLIT", raising=False)
+    B, N, K, D = 1, 5000, 4096, 128
+    x = torch.zeros((B, N, D), dtype=torch.float16, device="cuda")
+    c = torch.zeros((B, K, D), dtype=torch.float16, device="cuda")
+    csq = torch.zeros((B, K), dtype=torch.float32, device="cuda")
+    ids = torch.empty((B, N), dtype=torch.int32, device="cuda")
+    need = _lib.lib.fkc_euclid_assign_workspace_bytes(B, N, K, D, 1)
+    assert need >= 8 * B * N * 2
+    ws = torch.empty(need + 256, dtype=torch.uint8, device="cuda")
+    args = (x.data_ptr(), c.data_ptr(), None, csq.data_ptr(), ids.data_ptr(), B, N, K, D, 1)
+    stream = _lib.stream_of(x)
+    assert _lib.lib.fkc_euclid_assign_ws(*args, ws.data_ptr(), need - 1, stream) == 2
+    assert b"workspace" in _lib.lib.fkc_last_error()
+    assert _lib.lib.fkc_euclid_assign_ws(*args, None, 0, stream) == 2
+    assert _lib.lib.fkc_euclid_assign_ws(*args, ws.data_ptr() + 8, need, stream) == 2
+    assert _lib.lib.fkc_euclid_assign_ws(*args, ws.data_ptr(), need, stream) == 0
+    torch.cuda.synchronize()
+    assert (ids.cpu() == 0).all()  # all-zero data: every score ties, row 0 wins
+    assert _lib.lib.fkc_euclid_assign_workspace_bytes(1, 524288, 8192, 128, 1) == 0
+    assert _lib.lib.fkc_euclid_assign_workspace_bytes(1, 5000, 300, 128, 1) == 0
+
+
 @pytest.mark.parametrize("B,N,K,D", [(1, 4096, 64, 128), (2, 1000, 33, 37), (1, 513, 300, 16)])
 def test_fp32_route_matches_oracle(B, N, K, D):
     x, c = _data(B, N, K, D, "f32", seed=N + D)
