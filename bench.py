@@ -24,7 +24,8 @@ Reported:
                         the reference)
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--config c5]
-       python bench.py --report        per-config table (c1..c5): assign TFLOPS,
+       python bench.py --report        per-config table (c1..c5, c5s8 = c5 on one of 8
+                                       N-shards): assign TFLOPS,
                                        ms/iter (steady state and one-iteration
                                        call), roofline fraction ideal/measured
        python bench.py --gemm-peak     hipBLASLt GEMM TFLOP/s (practical
@@ -281,7 +282,7 @@ def main() -> int:
     ap.add_argument("--gemm-peak", action="store_true",
                     help="practical matrix-core ceiling: hipBLASLt GEMM TFLOP/s "
                          "(torch.matmul) on large fp16 / bf16 shapes")
-    ap.add_argument("--report", nargs="?", const="c1,c2,c3,c4,c5", default=None,
+    ap.add_argument("--report", nargs="?", const="c1,c2,c3,c4,c5,c5s8", default=None,
                     help="per-configuration table (comma-separated config names)")
     args = ap.parse_args()
 

@@ -49,6 +49,11 @@ CONFIGS = {
                  "mixture", seed=0, init_seed=100, per_batch_seed=True),
     "c5": Config("c5_f16_k8192_zipf", 1, 524288, 8192, 128, "f16", 10, 0.0,
                  "mixture", zipf=1.1),
+    # One GPU's share when c5 is sharded over N on 8 GPUs (65536 points, all
+    # 8192 centroids): the per-rank assign, sort and update at their real
+    # shape, without the per-iteration all-reduce of sums and counts.
+    "c5s8": Config("c5_share_of_8_f16_k8192_zipf", 1, 65536, 8192, 128, "f16",
+                   10, 0.0, "mixture", zipf=1.1),
 }
 
 
