@@ -253,6 +253,28 @@ def test_loop_sort_digit_counts(B, N, K, D, dtype):
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
+@pytest.mark.parametrize("B,N,K,dtype", [(1, 6000, 4500, "f16"), (2, 3000, 5000, "bf16")])
+def test_loop_with_sliced_assign(monkeypatch, B, N, K, dtype):
+    """Shapes with few points and many centroids slice K inside the loop's
+    assign (partial winners in the loop workspace): the loop, the per-op
+    path and the loop with slicing switched off (FKC_KSPLIT=1) agree bit for
+    bit over 3 iterations."""
+    from flash_kmeans_cuda import _lib, batch_kmeans_Euclid
+    monkeypatch.delenv("FKC_KSPLIT", raising=False)
+    dt = {"f16": 1, "bf16": 2}[dtype]
+    assert _lib.lib.fkc_euclid_assign_workspace_bytes(B, N, K, 128, dt) > 0
+    rng = np.random.default_rng(K)
+    x = O.from_f32(rng.standard_normal((B, N, 128)).astype(np.float32), dtype)
+    init = np.ascontiguousarray(x[:, :K])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it, verbose=True)
+    monkeypatch.setenv("FKC_KSPLIT", "1")
+    c = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it)
+    for r in (b, c):
+        assert torch.equal(a[0], r[0]) and torch.equal(a[1], r[1])
+
+
 def test_deterministic_loop():
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c3"]
