@@ -58,7 +58,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Compile-time tunables (defaults measured on MI355X at the benchmark
 // shapes): FKC_AB, minimum waves per SIMD asked of the register allocator
-// for the lighter variants; FKC_EXACT_MAX_K, largest K that tracks the exact
+// for the lighter variants (D = 33..64 asks 4: its four-tile variant then
+// fits 120 VGPRs instead of 129, 4 waves per SIMD instead of 3, and the c4
+// grid of 2048 workgroups runs in 2 rounds instead of 2.67: 101.8 -> 91.6
+// us at (8, 65536, 1024, 64) bf16; at D = 32 the same bound cost 5%); FKC_EXACT_MAX_K, largest K that tracks the exact
 // index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
 // FKC_KC_DMA, centroid rows per direct stage (D <= 128); FKC_KC_DMA8, the
 // same for the eight-tile variant (two workgroups per CU leave it twice the
@@ -147,6 +150,7 @@ __device__ inline void fold_exact(const f32x4& acc, float& best, int& bidx,
 template <int DT, int DS2, int PT, bool PAD, bool EXACT>
 __global__ void __launch_bounds__(THREADS,
                                   PT == 8 ? 2
+                                  : (DS2 == 2 && PT <= 4) ? 4
                                   : (PT * DS2 <= 16 && DS2 <= 9) ? FKC_AB
                                                                  : 1)
 assign_mfma_kernel(const uint16_t* __restrict__ x,
