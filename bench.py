@@ -47,6 +47,8 @@ sys.path.insert(0, os.path.join(HERE, "flash-kmeans-cuda_amd"))
 sys.path.insert(0, HERE)
 
 PEAK_TFLOPS_F16 = 2500.0          # MI355X dense fp16/bf16 MFMA
+PEAK_TFLOPS_F32 = 157.3           # MI355X fp32 (the fp32 route runs on the VALU)
+METRIC_C5 = "assign TFLOPS + end-to-end ms/iter at (1,524K,8192,128) fp16, 1 MI355X"
 PROFILE_PERIOD = 5                # event-time the assign of every 5th timed iteration
 PEAK_HBM_GBS = 8000.0
 REF_MS_PER_ITER = {"c5": 6.179, "c3": 0.489, "c2": 0.129}   # README.md:31-34 (RTX 4090)
@@ -358,8 +360,13 @@ def main() -> int:
     disagree = int((ids_now[:, sub] != ref).sum())
 
     traffic = _traffic_from_profiles(args.config)
+    f32 = cfg.dtype == "f32"
+    peak = PEAK_TFLOPS_F32 if f32 else PEAK_TFLOPS_F16
+    metric = (METRIC_C5 if args.config == "c5" else
+              f"assign TFLOPS + end-to-end ms/iter at ({cfg.B},{cfg.N},{cfg.K},{cfg.D}) "
+              f"{ {'f32': 'fp32', 'f16': 'fp16'}.get(cfg.dtype, cfg.dtype)}, 1 MI355X")
     line = {
-        "metric": "assign TFLOPS + end-to-end ms/iter at (1,524K,8192,128) fp16, 1 MI355X",
+        "metric": metric,
         "value": round(ms_per_step, 5),
         "unit": "ms/iter",
         "n_gpus": 1,
@@ -385,11 +392,11 @@ def main() -> int:
                                if args.config in REF_ASSIGN_TFLOPS else None),
         "ms_per_iter_ref_method": round(min(one), 5),
         "roofline": {
-            "bound": "mfma",
+            "bound": "valu" if f32 else "mfma",
             "achieved": round(assign_tflops, 2),
-            "peak": PEAK_TFLOPS_F16,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(assign_tflops / PEAK_TFLOPS_F16, 4),
+            "frac": round(assign_tflops / peak, 4),
             "traffic": traffic,
         },
         "parity_sample": {"points": int(sub.size), "label_disagreements": disagree},

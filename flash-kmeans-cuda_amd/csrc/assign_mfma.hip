@@ -46,6 +46,8 @@
 #include "fkc_internal.hpp"
 
 #include <hip/hip_ext.h>
+
+#include <algorithm>
 #include <math.h>
 
 namespace fkc {
@@ -808,7 +810,8 @@ struct Plan {
 // N = 131072, K = 2048, D = 128 four slices of 512 rows took 0.124 ms
 // against 0.073 ms unsliced; at N = 80000, K = 70000, D = 16 four slices
 // took 0.376 ms against 0.756 ms, and at N = 8192, K = 65536, D = 128
-// eight slices 0.150 ms against 0.531 ms.  FKC_KSPLIT forces S.
+// eight slices 0.150 ms against 0.531 ms.  At D = 97..128 the slices fill
+// one round of resident workgroups (below).  FKC_KSPLIT forces S.
 static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
                         bool can_slice) {
   Plan p;
@@ -827,9 +830,17 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   int pt = p.pt;
   if (ntiles_override() == 0) pt = p.ds2 <= 4 ? 4 : p.ds2 <= 8 ? 2 : 1;
   const int64_t tiles = grid_wgs(pt, B, N);
-  const int64_t want = fill_wgs(pt, p.ds2, p.exact);
   int64_t S = ksplit_override();
-  if (S == 0) {
+  if (S == 0 && pt == 4 && p.ds2 == 4) {
+    // D = 97..128: as many slices as fit one round of the 167-VGPR
+    // variant's 768 resident workgroups (3 per CU).  One round, not two: at
+    // N = 65536, K = 8192 three slices took 0.117 ms, four 0.122, none
+    // 0.121; at N = 32768, K = 16384 six 0.123, three 0.138, none 0.220;
+    // at N = 131072, K = 4096 two slices (two rounds) lost 6%.
+    S = std::min<int64_t>(768 / tiles, K / FKC_SLICE_MIN_ROWS);
+    if (S <= 1) return p;
+  } else if (S == 0) {
+    const int64_t want = fill_wgs(pt, p.ds2, p.exact);
     if (tiles >= want) return p;
     S = 1;
     while (tiles * S < want && K / (2 * S) >= FKC_SLICE_MIN_ROWS) S *= 2;

@@ -146,12 +146,14 @@ def test_empty_inputs_are_no_ops():
 
 def test_assign_slice_plan(monkeypatch):
     """Which shapes slice K and how large the partial-winner workspace is
-    (8 bytes per point and slice, each half 256-byte aligned).  None where an
-    unsliced grid fills the chip: the benchmark shape (c5, 1024 eight-tile
-    workgroups), c3 and c5's one-GPU share of eight (four tiles on 512 / 256
-    workgroups), c4 (2048 four-tile workgroups); none for K <= 512 (exact
-    in-loop index), the fp32 route, or slices shorter than 2048 rows.
-    FKC_KSPLIT forces a count."""
+    (8 bytes per point and slice, each half 256-byte aligned).  At D = 128
+    the four-tile workgroups of all slices fill one round of 768 (3 per CU)
+    with slices of >= 2048 rows: none for the benchmark shape (c5, 1024
+    eight-tile workgroups) or c3 (512 four-tile workgroups, slices would be
+    1024 rows), 3 for c5's one-GPU share of eight (256 workgroups).  Other
+    widths slice only when no unsliced grid fills the chip: none for c4
+    (2048 workgroups).  None for K <= 512 (exact in-loop index), the fp32
+    route, or slices shorter than 2048 rows.  FKC_KSPLIT forces a count."""
     from flash_kmeans_cuda import _lib
     monkeypatch.delenv("FKC_KSPLIT", raising=False)
     monkeypatch.delenv("FKC_NTILES", raising=False)
@@ -159,7 +161,8 @@ def test_assign_slice_plan(monkeypatch):
     half = lambda n: (n * 4 + 255) // 256 * 256
     assert f(1, 524288, 8192, 128, 1) == 0
     assert f(1, 131072, 2048, 128, 1) == 0
-    assert f(1, 65536, 8192, 128, 2) == 0
+    assert f(1, 65536, 8192, 128, 2) == 2 * half(3 * 65536)   # 2816-row slices
+    assert f(1, 32768, 16384, 128, 1) == 2 * half(6 * 32768)
     assert f(1, 32768, 256, 128, 1) == 0
     assert f(8, 65536, 1024, 64, 2) == 0
     assert f(1, 131072, 2048, 128, 0) == 0
