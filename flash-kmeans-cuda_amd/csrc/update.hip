@@ -187,6 +187,8 @@ __device__ inline void finalize_row(const float* row, int cnt,
   finish_norms(sq, sh, csq, shift, lane);
 }
 
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
 template <int DT, int VEC, int NI, bool INDEXED>
 __global__ void __launch_bounds__(UT)
 update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
@@ -372,6 +374,10 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     for (int v = 0; v < VEC; ++v) acc[i][v] = 0.f;
 
   using R = typename RC::T;
+  // The full unroll asked here exceeds the unroller's size limit and is not
+  // done (clang warns; the warning is silenced around this kernel), yet the
+  // code built with the request ran 9% faster at N = 524288, D = 128 than
+  // with `unroll 1` or `unroll 2` (34.8 vs 37.9 / 37.3 us).
 #pragma unroll
   for (int q = 0; q < UR_MAX / RB; ++q) {
     const int r0 = q * RB;  // first unit row of the batch
@@ -454,6 +460,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     m[UnitMeta::THROUGH] = through;
   }
 }
+#pragma clang diagnostic pop
 
 // Wave-cooperative ordered sum of partial rows (D fp32 each):
 //   out[c] = first[c] + row(0)[c] + ... + row(n-1)[c]   (first may be null)
