@@ -360,7 +360,8 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   // restart from zero if the row starts a run.  The runs that closed in the
   // sub-batch are then flushed from their slots by a loop with a single
   // flush site.  (A per-row branch to a flush, even one that is rarely
-  // taken, doubled the kernel's time.)
+  // taken, doubled the kernel's time; sub-batches without a run start take
+  // a plain-add path instead.)
   constexpr int RB = 32 / NI;          // rows in flight per wave
   constexpr int FH = 16 / NI;          // rows per folded sub-batch
   constexpr int SL = NI * VEC;         // floats per lane per slot
@@ -404,6 +405,26 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
       if (s0 >= urows) break;
       const uint64_t cm = starts[s0 >> 6] >> (s0 & 63);
       const uint32_t hb = (uint32_t)cm & ((1u << FH) - 1u);  // run starts
+      // A sub-batch with no run start and every row in use (most of them:
+      // runs are long) only adds its rows, the same additions as below
+      // without the slot stores and selects.  The branch is wave-uniform and
+      // taken per sub-batch, not per row (measured at N = 524288, D = 128:
+      // 34.4 -> 31.5 us; at c4's 8 x 65536 x 64: 32.8 -> 30.2 us).
+      const uint32_t um = (okm >> (h * FH)) & ((1u << FH) - 1u);
+      if (hb == 0u && um == (1u << FH) - 1u) {
+#pragma unroll
+        for (int t = 0; t < FH; ++t) {
+          const int jj = h * FH + t;
+#pragma unroll
+          for (int i = 0; i < NI; ++i) {
+            float f[VEC];
+            RC::cvt(raw[jj][i], f);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) acc[i][v] = acc[i][v] + f[v];
+          }
+        }
+        continue;
+      }
       int nseg = 0;
 #pragma unroll
       for (int t = 0; t < FH; ++t) {
