@@ -236,6 +236,9 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     col[i] = cbase + (lane + 64 * i) * VEC;
     cok[i] = col[i] < D;  // D % VEC == 0, so the whole vector is in range
   }
+  int lcol[NI];  // the column each lane loads: its own, or 0 past D
+#pragma unroll
+  for (int i = 0; i < NI; ++i) lcol[i] = cok[i] ? col[i] : 0;
 
   using Acc = float[NI][VEC];
   int tail_id = 0, tail_len = 0, head_len = 0, through = 0;
@@ -395,9 +398,11 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
       const bool rok = r < urows && (uint32_t)row < (uint32_t)N;
       okm |= rok ? (1u << jj) : 0u;
       const T* xr = xb + (size_t)(rok ? row : 0) * D;
+      // Unconditional, from an in-bounds column: a lane past D loads column
+      // 0 and its sums are never stored (every store checks cok), so no
+      // per-row branch on the lane's column is needed.
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
-        raw[jj][i] = cok[i] ? RC::load(xr + col[i]) : RC::zero();
+      for (int i = 0; i < NI; ++i) raw[jj][i] = RC::load(xr + lcol[i]);
     }
 #pragma unroll
     for (int h = 0; h < RB / FH; ++h) {
