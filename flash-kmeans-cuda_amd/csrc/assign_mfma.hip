@@ -65,7 +65,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // grid of 2048 workgroups runs in 2 rounds instead of 2.67: 101.8 -> 91.6
 // us at (8, 65536, 1024, 64) bf16; at D = 32 the same bound cost 5%); FKC_EXACT_MAX_K, largest K that tracks the exact
 // index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
-// FKC_KC_DMA, centroid rows per direct stage (D <= 128); FKC_KC_DMA8, the
+// FKC_KC_DMA, centroid rows per direct stage at D = 97..128 (x4 at D = 32,
+// x2 at D = 64); FKC_KC_DMA8, the
 // same for the eight-tile variant (two workgroups per CU leave it twice the
 // LDS); FKC_SLICE_MIN_ROWS, the shortest centroid slice; FKC_SCHED_GROUPS,
 // LDS-read / MFMA / VALU ordering hints in the direct-stage loop.
@@ -249,7 +250,15 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // stays below K).  Only K < KCD clamps rows to K-1.  c_sq lands raw and
     // each wave scales (and masks past K) its own share once its loads are
     // in, before the barrier.
-    constexpr int KCD0 = PT == 8 ? FKC_KC_DMA8 : DS2 <= 4 ? FKC_KC_DMA : 64;
+    // Stage rows: FKC_KC_DMA rows at D = 97..128; the narrow widths keep
+    // the same 16 KB per stage with more rows (D = 32: 256 rows, 0.026 ->
+    // 0.021 ms at (2, 30000, 2000, 32); D = 64: 128 rows, ~1%), so a stage
+    // still spans enough matrix work to hide its barrier.
+    constexpr int KCD0 = PT == 8    ? FKC_KC_DMA8
+                         : DS2 == 1 ? 4 * FKC_KC_DMA
+                         : DS2 == 2 ? 2 * FKC_KC_DMA
+                         : DS2 <= 4 ? FKC_KC_DMA
+                                    : 64;
     constexpr int KCD = (KCD0 * DP * 2) % (THREADS * 16) == 0 ? KCD0 : 64;
     constexpr int ROWB = DP * 2;
     constexpr int STAGE = KCD * ROWB;

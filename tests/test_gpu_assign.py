@@ -54,6 +54,7 @@ MFMA_CASES = [
     (1, 100, 8, 64), (1, 257, 16, 128), (1, 1024, 1, 64), (1, 1024, 63, 64),
     (1, 1024, 65, 64), (1, 1024, 32, 256), (3, 2048, 32, 64),       # test_shapes
     (1, 256, 2048, 128), (1, 777, 129, 128),
+    (1, 3000, 1000, 32), (2, 2000, 700, 64), (1, 1500, 5000, 32),  # re-score, partial last stage
 ]
 
 
