@@ -611,25 +611,35 @@ update_merge_kernel(const float* __restrict__ part,
   const int u = blockIdx.x * (UT / 64) + wave;
   if (u >= nunits) return;
   const int32_t* mb = meta + (size_t)b * nunits * 4;
-  const int tail_len = mb[(size_t)u * 4 + UnitMeta::TAIL_LEN];
+  // Lane j loads the whole record of unit u + j (one 16-byte load): lane 0
+  // gives the tail, lanes 1.. the continuation flags and head lengths of the
+  // units after u, so the common case needs no further metadata round trip.
+  const int vj = u + lane;
+  const int4 mv = vj < nunits ? reinterpret_cast<const int4*>(mb)[vj]
+                              : int4{0, 0, 0, 0};
+  static_assert(UnitMeta::TAIL_ID == 0 && UnitMeta::TAIL_LEN == 1 &&
+                    UnitMeta::HEAD_LEN == 2 && UnitMeta::THROUGH == 3,
+                "int4 view of the unit record");
+  const int tail_len = __builtin_amdgcn_readfirstlane(mv.y);
   if (tail_len == 0) return;
-  const int id = mb[(size_t)u * 4 + UnitMeta::TAIL_ID];
+  const int id = __builtin_amdgcn_readfirstlane(mv.x);
   if ((uint32_t)id >= (uint32_t)K) return;
   const int32_t* bmb = bmeta + (size_t)b * nblocks * 2;
 
   // The run continues through units u+1 .. e (e = first unit after u that
   // is not wholly inside the run; the last unit never is, so e exists).
   // Items, in order: heads of units u+1 .. min(e, end of u's block), then
-  // full blocks, then heads of the units of the block holding e.
+  // full blocks, then heads of the units of the block holding e.  Units
+  // u+1 .. bend-1 are lanes 1 .. bend-1-u (at most 63).
   const int bend = min((u / UB + 1) * UB, nunits);
   int n1, nblk = 0, n3 = 0, beta0 = u / UB + 1, v3 = 0;
+  bool simple = false;  // the run ends inside u's block: lengths from mv
   {
-    const int v = u + 1 + lane;
-    const bool stop =
-        v < bend && mb[(size_t)v * 4 + UnitMeta::THROUGH] == 0;
+    const bool stop = lane >= 1 && vj < bend && mv.w == 0;
     const uint64_t m = __builtin_amdgcn_ballot_w64(stop);
     if (m) {
-      n1 = __builtin_ctzll(m) + 1;  // units u+1 .. u+n1
+      n1 = __builtin_ctzll(m);  // units u+1 .. u+n1 (lanes 1 .. n1)
+      simple = true;
     } else {
       n1 = bend - (u + 1);
       int be = -1;
@@ -657,8 +667,8 @@ update_merge_kernel(const float* __restrict__ part,
     return pb + ((size_t)(v3 + i - n1 - nblk) * 2 + 0) * D;
   };
   // Row count: lanes over items, then a wave sum (integer, order-free).
-  int l = 0;
-  for (int i = lane; i < n; i += 64) {
+  int l = simple ? (lane >= 1 && lane <= n1 ? mv.z : 0) : 0;
+  for (int i = simple ? n : lane; i < n; i += 64) {
     if (i < n1)
       l += mb[(size_t)(u + 1 + i) * 4 + UnitMeta::HEAD_LEN];
     else if (i < n1 + nblk)
