@@ -253,7 +253,7 @@ def test_loop_sort_digit_counts(B, N, K, D, dtype):
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
-@pytest.mark.parametrize("B,N,K,dtype", [(1, 6000, 4500, "f16"), (2, 3000, 5000, "bf16")])
+@pytest.mark.parametrize("B,N,K,dtype", [(1, 6000, 4500, "f16"), (2, 6000, 5000, "bf16")])
 def test_loop_with_sliced_assign(monkeypatch, B, N, K, dtype):
     """Shapes with few points and many centroids slice K inside the loop's
     assign (partial winners in the loop workspace): the loop, the per-op
