@@ -12,6 +12,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
+#include <mutex>
 #include <vector>
 
 #include "fkc_internal.hpp"
@@ -65,14 +67,19 @@ int sort_tile_override() {
 
 // ------------------------------------------------------------- profiling
 namespace {
+// Process-wide profiling state.  The loop reads `period` without a lock;
+// the event lists and totals are only touched under `mu`, so calls from
+// several threads are safe (their timed launches are pooled).
 struct Profile {
-  int period = 0;  // time the assign of every period-th iteration; 0: off
+  std::atomic<int> period{0};  // time the assign of every period-th iteration; 0: off
+  std::mutex mu;
   std::vector<hipEvent_t> starts, stops;
   double total_ms = 0.0;
   int64_t launches = 0;
 };
 Profile g_prof;
 
+// Caller holds g_prof.mu.
 void prof_clear_events() {
   for (auto e : g_prof.starts) (void)hipEventDestroy(e);
   for (auto e : g_prof.stops) (void)hipEventDestroy(e);
@@ -370,10 +377,15 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
     // and invalidate) an event otherwise implies, which cost ~5 us around
     // each assign.
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (g_prof.period > 0 && it % g_prof.period == 0) {
-      if (hipEventCreateWithFlags(&e0, hipEventDisableSystemFence) != hipSuccess ||
-          hipEventCreateWithFlags(&e1, hipEventDisableSystemFence) != hipSuccess)
+    const int period = g_prof.period.load(std::memory_order_relaxed);
+    if (period > 0 && it % period == 0) {
+      if (hipEventCreateWithFlags(&e0, hipEventDisableSystemFence) != hipSuccess)
         return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: profiling event creation failed");
+      if (hipEventCreateWithFlags(&e1, hipEventDisableSystemFence) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: profiling event creation failed");
+      }
+      std::lock_guard<std::mutex> lock(g_prof.mu);
       g_prof.starts.push_back(e0);
       g_prof.stops.push_back(e1);
     }
@@ -420,13 +432,15 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
 }
 
 void fkc_profile_enable(int enable) {
-  g_prof.period = enable > 0 ? enable : 0;
+  std::lock_guard<std::mutex> lock(g_prof.mu);
+  g_prof.period.store(enable > 0 ? enable : 0, std::memory_order_relaxed);
   prof_clear_events();
   g_prof.total_ms = 0.0;
   g_prof.launches = 0;
 }
 
 int fkc_profile_assign_ms(double* total_ms, int64_t* launches) {
+  std::lock_guard<std::mutex> lock(g_prof.mu);
   double tot = 0.0;
   for (size_t i = 0; i < g_prof.starts.size(); ++i) {
     if (hipEventSynchronize(g_prof.stops[i]) != hipSuccess)

@@ -209,6 +209,8 @@ FKC_CAPI int fkc_kmeans_lloyd(const void* x, void* centroids,
  * microseconds, so k > 1 keeps that out of most iterations); enable = 0
  * turns it off.  fkc_profile_assign_ms() synchronises on the recorded events
  * and returns the summed assignment time in ms and the timed launch count.
+ * The hook is process-wide: calls from several threads are safe and their
+ * timed launches are pooled.
  */
 FKC_CAPI void fkc_profile_enable(int enable);
 FKC_CAPI int fkc_profile_assign_ms(double* total_ms, int64_t* launches);
