@@ -13,6 +13,8 @@ import os
 import torch  # noqa: F401  (loads torch's HIP runtime first)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
+# FKC_LIBRARY: path of another build of libfkc.so (same-box A/B runs of two
+# builds); unset, the in-tree library next to this package is loaded.
 LIB_PATH = os.environ.get("FKC_LIBRARY", os.path.join(_HERE, "libfkc.so"))
 
 FKC_OK = 0
