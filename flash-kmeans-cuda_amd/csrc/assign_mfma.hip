@@ -27,8 +27,9 @@
 // issues under this block's fold).  At the end the four lanes that share a
 // point (l, l+16, l+32, l+48) merge with the lowest-index rule, and the
 // winner's four candidate rows are scored again by the same MFMA chain to
-// pick the first maximal one.  For K <= FKC_EXACT_MAX_K the loop tracks the
-// exact index instead (the re-score would cost more than it saves).
+// pick the first maximal one.  For K <= FKC_EXACT_MAX_K (1024 at D <= 64)
+// the loop tracks the exact index instead (the re-score would cost more than
+// it saves).
 // Feature widths that are not a multiple of 32 are zero-padded in registers
 // and LDS (zeros add nothing to a dot product).
 //
@@ -63,8 +64,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // for the lighter variants (D = 33..64 asks 4: its four-tile variant then
 // fits 120 VGPRs instead of 129, 4 waves per SIMD instead of 3, and the c4
 // grid of 2048 workgroups runs in 2 rounds instead of 2.67: 101.8 -> 91.6
-// us at (8, 65536, 1024, 64) bf16; at D = 32 the same bound cost 5%); FKC_EXACT_MAX_K, largest K that tracks the exact
-// index in the loop; FKC_USE_DMA, direct global->LDS stages where eligible;
+// us at (8, 65536, 1024, 64) bf16; at D = 32 the same bound cost 5%);
+// FKC_EXACT_MAX_K (FKC_EXACT_MAX_K_NARROW at D <= 64), largest K that
+// tracks the exact index in the loop; FKC_USE_DMA, direct global->LDS
+// stages where eligible;
 // FKC_KC_DMA, centroid rows per direct stage at D = 97..128 (x4 at D = 32,
 // x2 at D = 64); FKC_KC_DMA8, the
 // same for the eight-tile variant (two workgroups per CU leave it twice the
@@ -75,6 +78,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #endif
 #ifndef FKC_EXACT_MAX_K
 #define FKC_EXACT_MAX_K 512
+#endif
+#ifndef FKC_EXACT_MAX_K_NARROW
+#define FKC_EXACT_MAX_K_NARROW 1024
 #endif
 #ifndef FKC_USE_DMA
 #define FKC_USE_DMA 1
@@ -827,8 +833,12 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   p.ds2 = (int)((D + 31) / 32);
   p.pad = D != 32 * p.ds2;
   // Re-scoring the winning block costs about one 16-centroid block per point
-  // tile; below this K the exact in-loop index is cheaper.
-  p.exact = K <= FKC_EXACT_MAX_K;
+  // tile and a round trip for the candidate rows; below this K the exact
+  // in-loop index is cheaper.  At D <= 64 (fewer MFMAs per block to hide
+  // the fold) up to K = 1024: (8, 65536, 1024, 64) bf16 0.0817 -> 0.0766
+  // ms, (1, 131072, 1024, 64) 0.0282 -> 0.0263 ms; at D = 128 the exact
+  // fold lost at K = 2048 (+8%) and gained 1% at K = 1024.
+  p.exact = K <= FKC_EXACT_MAX_K || (p.ds2 <= 2 && K <= FKC_EXACT_MAX_K_NARROW);
   p.pt = choose_pt(p.ds2, p.pad, p.exact, B, N);
   p.S = 1;
   p.kspan = (int)K;
