@@ -141,9 +141,12 @@ def test_tiny_golden_fixtures_on_gpu():
 
 @pytest.mark.parametrize("B,N,K,D", [(1, 100, 8, 64), (1, 257, 16, 128), (1, 1024, 1, 64),
                                      (1, 1024, 63, 64), (1, 1024, 65, 64), (1, 1024, 32, 256),
-                                     (3, 2048, 32, 64)])
+                                     (3, 2048, 32, 64),
+                                     # degenerate: K > N (duplicate initial centroids,
+                                     # empty clusters), one point, K = N, narrowest width
+                                     (1, 100, 500, 64), (2, 1, 4, 8), (1, 7, 1, 8), (1, 3, 3, 8)])
 def test_shapes_contract(B, N, K, D):
-    """tests/test_shapes.py:11-31 of the reference."""
+    """tests/test_shapes.py:11-31 of the reference, plus degenerate shapes."""
     from flash_kmeans_cuda import batch_kmeans_Euclid
     x = torch.randn(B, N, D, device="cuda", dtype=torch.float16)
     ids, cents, n_iters = batch_kmeans_Euclid(x, K, max_iters=3, tol=0.0)
@@ -151,6 +154,11 @@ def test_shapes_contract(B, N, K, D):
     assert cents.shape == (B, K, D) and cents.dtype == torch.float16
     assert n_iters == 3
     assert (ids >= 0).all() and (ids < K).all()
+    assert torch.isfinite(cents.float()).all()
+    # every centroid is a mean of points or an initial point: inside the data's box
+    lo = x.float().amin(dim=1, keepdim=True) - 1e-2
+    hi = x.float().amax(dim=1, keepdim=True) + 1e-2
+    assert ((cents.float() >= lo) & (cents.float() <= hi)).all()
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
