@@ -333,11 +333,15 @@ size_t fkc_kmeans_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,
   return total;
 }
 
-int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
-                     int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
-                     int max_iters, float tol, void* workspace,
-                     size_t workspace_bytes, fkc_stream_t stream,
-                     int32_t* n_iters_dev, int32_t* n_iters_host) {
+}  // extern "C"
+
+namespace {
+// fkc_kmeans_lloyd (init == centroids) and fkc_kmeans_lloyd_from.
+int lloyd_impl(const void* x, const void* init, void* centroids,
+               int32_t* cluster_ids, int64_t B, int64_t N, int64_t K,
+               int64_t D, int dtype, int max_iters, float tol, void* workspace,
+               size_t workspace_bytes, fkc_stream_t stream,
+               int32_t* n_iters_dev, int32_t* n_iters_host) {
   g_err[0] = 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (int rc = shape_ok(B, N, K, D, "kmeans_lloyd")) return rc;
@@ -345,12 +349,21 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
   if (max_iters < 0) return fail(FKC_ERR_INVALID, "kmeans_lloyd: max_iters < 0");
   if (B == 0 || N == 0 || max_iters == 0) {
     if (n_iters_host) *n_iters_host = (B == 0 || N == 0) ? max_iters : 0;
+    // The centroids returned are the initial ones.
+    if (B > 0 && init != centroids) {
+      if (!init || !centroids)
+        return fail(FKC_ERR_INVALID, "kmeans_lloyd: null pointer argument");
+      const size_t esz = dtype == FKC_F32 ? 4 : 2;
+      if (hipMemcpyAsync(centroids, init, (size_t)B * K * D * esz,
+                         hipMemcpyDeviceToDevice, s) != hipSuccess)
+        return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: copy of the initial centroids failed");
+    }
     if (n_iters_dev)
       return launch_fill_i32(n_iters_dev, (B == 0 || N == 0) ? max_iters : 0,
                              1, s);
     return FKC_OK;
   }
-  if (!x || !centroids || !cluster_ids)
+  if (!x || !init || !centroids || !cluster_ids)
     return fail(FKC_ERR_INVALID, "kmeans_lloyd: null pointer argument");
   size_t need = 0;
   carve_loop(nullptr, B, N, K, D, dtype, max_iters, &need);
@@ -364,11 +377,19 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
 
   const bool check = tol > 0.f;
   const int32_t* ctrl = check ? L.ctrl : nullptr;
-  int rc = launch_fill_i32(L.ctrl, 0, 4, s);
-  if (!rc && check) rc = launch_fill_f32(L.shift, 0.f, max_iters, s);
-  if (!rc) rc = label_sort_reset(L.sort_ws, B, N, K, s);
+  // One prologue launch: copy of the initial centroids (when separate),
+  // their c_sq, and the zeroing of the control words, the sort's first
+  // phase and the shift slots.
+  ZeroFill zf;
+  zf.z0 = L.ctrl;
+  zf.n0 = 4;
+  label_sort_reset_region(L.sort_ws, B, N, K, &zf.z1, &zf.n1);
+  if (check) {
+    zf.z2 = L.shift;
+    zf.n2 = max_iters;
+  }
+  int rc = launch_lloyd_prologue(init, centroids, L.c_sq, B * K, D, dtype, zf, s);
   if (!rc && L.x_sq) rc = launch_row_sqnorm(x, L.x_sq, B * N, D, dtype, nullptr, s);
-  if (!rc) rc = launch_row_sqnorm(centroids, L.c_sq, B * K, D, dtype, nullptr, s);
   if (rc) return rc;
 
   for (int it = 0; it < max_iters; ++it) {
@@ -429,6 +450,30 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
     }
   }
   return FKC_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
+                     int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
+                     int max_iters, float tol, void* workspace,
+                     size_t workspace_bytes, fkc_stream_t stream,
+                     int32_t* n_iters_dev, int32_t* n_iters_host) {
+  return lloyd_impl(x, centroids, centroids, cluster_ids, B, N, K, D, dtype,
+                    max_iters, tol, workspace, workspace_bytes, stream,
+                    n_iters_dev, n_iters_host);
+}
+
+int fkc_kmeans_lloyd_from(const void* x, const void* init_centroids,
+                          void* centroids, int32_t* cluster_ids, int64_t B,
+                          int64_t N, int64_t K, int64_t D, int dtype,
+                          int max_iters, float tol, void* workspace,
+                          size_t workspace_bytes, fkc_stream_t stream,
+                          int32_t* n_iters_dev, int32_t* n_iters_host) {
+  return lloyd_impl(x, init_centroids, centroids, cluster_ids, B, N, K, D,
+                    dtype, max_iters, tol, workspace, workspace_bytes, stream,
+                    n_iters_dev, n_iters_host);
 }
 
 void fkc_profile_enable(int enable) {

@@ -79,6 +79,50 @@ __global__ void iota_i32_kernel(int32_t* p, int64_t B, int64_t N) {
   for (int64_t j = i; j < B * N; j += stride) p[j] = (int32_t)(j % N);
 }
 
+// Lloyd loop prologue in one launch.  Row blocks (four rows each, one wave
+// per row) copy the initial centroids into the loop's centroid buffer when
+// the two differ and write their squared norms with the column order and
+// wave reduction of row_sqnorm_kernel (the same bits); the blocks after
+// them zero the loop's control words, the label sort's error word and
+// first digit counts and, with a tolerance, the shift slots.
+template <int DT>
+__global__ void __launch_bounds__(256)
+lloyd_prologue_kernel(const typename Elem<DT>::T* __restrict__ init,
+                      typename Elem<DT>::T* __restrict__ cent,
+                      float* __restrict__ c_sq, int64_t rows, int D,
+                      int32_t* __restrict__ z0, int64_t n0,
+                      int32_t* __restrict__ z1, int64_t n1,
+                      float* __restrict__ z2, int64_t n2) {
+  using E = Elem<DT>;
+  const int64_t row_blocks = (rows + 3) / 4;
+  if ((int64_t)blockIdx.x >= row_blocks) {
+    const int64_t i0 = ((int64_t)blockIdx.x - row_blocks) * 256 + threadIdx.x;
+    const int64_t stride = ((int64_t)gridDim.x - row_blocks) * 256;
+    for (int64_t i = i0; i < n0; i += stride) z0[i] = 0;
+    for (int64_t i = i0; i < n1; i += stride) z1[i] = 0;
+    for (int64_t i = i0; i < n2; i += stride) z2[i] = 0.f;
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const typename E::T* src = init + row * D;
+  typename E::T* dst = cent + row * D;
+  const bool copy = init != cent;
+  const int vec = row_vec(D);
+  float acc = 0.f;
+  for (int c = vec * lane; c < D; c += vec * 64) {
+    for (int v = 0; v < vec; ++v) {
+      const typename E::T e = src[c + v];
+      if (copy) dst[c + v] = e;
+      const float f = E::load(e);
+      acc = fmaf(f, f, acc);
+    }
+  }
+  acc = row_sum(acc);
+  if (lane == 0) c_sq[row] = acc;
+}
+
 // ctrl[0] = converged flag, ctrl[1] = iterations run.  Runs after the
 // finalize of iteration `it`, single thread.
 __global__ void converge_check_kernel(const float* shift, int it, float tol,
@@ -126,6 +170,36 @@ int launch_finalize(const float* sums, const int32_t* counts, const void* old,
                                          shift_out, rows, D, ctrl, s);
   }
   return fail(FKC_ERR_INVALID, "centroid_finalize: unknown dtype %d", dtype);
+}
+
+template <int DT>
+int launch_prologue_t(const void* init, void* cent, float* c_sq, int64_t rows,
+                      int64_t D, const ZeroFill& f, hipStream_t s) {
+  using T = typename Elem<DT>::T;
+  const int64_t nz = f.n0 > f.n1 ? (f.n0 > f.n2 ? f.n0 : f.n2)
+                                 : (f.n1 > f.n2 ? f.n1 : f.n2);
+  const int64_t zb = nz > 0 ? (nz + 255) / 256 < 64 ? (nz + 255) / 256 : 64 : 0;
+  const int64_t blocks = (rows + 3) / 4 + zb;
+  if (blocks <= 0) return FKC_OK;
+  hipLaunchKernelGGL((lloyd_prologue_kernel<DT>), dim3((unsigned)blocks),
+                     dim3(256), 0, s, static_cast<const T*>(init),
+                     static_cast<T*>(cent), c_sq, rows, (int)D, f.z0, f.n0,
+                     f.z1, f.n1, f.z2, f.n2);
+  return check_launch("lloyd_prologue");
+}
+
+int launch_lloyd_prologue(const void* init, void* cent, float* c_sq,
+                          int64_t rows, int64_t D, int dtype,
+                          const ZeroFill& f, hipStream_t s) {
+  switch (dtype) {
+    case FKC_F32:
+      return launch_prologue_t<FKC_F32>(init, cent, c_sq, rows, D, f, s);
+    case FKC_F16:
+      return launch_prologue_t<FKC_F16>(init, cent, c_sq, rows, D, f, s);
+    case FKC_BF16:
+      return launch_prologue_t<FKC_BF16>(init, cent, c_sq, rows, D, f, s);
+  }
+  return fail(FKC_ERR_INVALID, "kmeans_lloyd: unknown dtype %d", dtype);
 }
 
 int launch_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s) {

@@ -77,6 +77,10 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
                       void* ws, size_t ws_bytes, const int32_t* ctrl,
                       hipStream_t s, int phase = -1);
 int label_sort_reset(void* ws, int64_t B, int64_t N, int64_t K, hipStream_t s);
+// The int32 region label_sort_reset zeroes (for fusing it into another
+// launch): *p, *n (n = 0 when B * N == 0).
+void label_sort_reset_region(void* ws, int64_t B, int64_t N, int64_t K,
+                             int32_t** p, int64_t* n);
 // FKC_SORT_TILE=256|512|1024|2048|4096: keys per sort tile; 0 = auto.
 int sort_tile_override();
 
@@ -113,6 +117,20 @@ int launch_finalize(const float* sums, const int32_t* counts, const void* old,
 
 // ---------------------------------------------------------------- misc
 int launch_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
+// Zero-fills fused into the Lloyd prologue (null pointer / zero count: none).
+struct ZeroFill {
+  int32_t* z0 = nullptr;
+  int64_t n0 = 0;
+  int32_t* z1 = nullptr;
+  int64_t n1 = 0;
+  float* z2 = nullptr;
+  int64_t n2 = 0;
+};
+// One launch: cent = init (when the pointers differ), c_sq = row squared
+// norms of init (the bits of launch_row_sqnorm), and the zero-fills.
+int launch_lloyd_prologue(const void* init, void* cent, float* c_sq,
+                          int64_t rows, int64_t D, int dtype,
+                          const ZeroFill& f, hipStream_t s);
 // p[b*N + n] = n for every batch row b.
 int launch_iota_i32(int32_t* p, int64_t B, int64_t N, hipStream_t s);
 int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);

@@ -443,9 +443,20 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
 
 int label_sort_reset(void* ws, int64_t B, int64_t N, int64_t K,
                      hipStream_t s) {
-  if (B == 0 || N == 0) return FKC_OK;
+  int32_t* p = nullptr;
+  int64_t n = 0;
+  label_sort_reset_region(ws, B, N, K, &p, &n);
+  return launch_fill_i32(p, 0, n, s);
+}
+
+void label_sort_reset_region(void* ws, int64_t B, int64_t N, int64_t K,
+                             int32_t** p, int64_t* n) {
+  *p = nullptr;
+  *n = 0;
+  if (B == 0 || N == 0) return;
   SortBufs w = carve_sort(ws, B, N, K, nullptr);
-  return launch_fill_i32(w.err, 0, 64 + w.gphase, s);
+  *p = w.err;
+  *n = 64 + w.gphase;
 }
 
 }  // namespace fkc

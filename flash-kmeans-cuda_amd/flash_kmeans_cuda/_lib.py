@@ -41,6 +41,7 @@ SIGNATURES = {
     "fkc_centroid_finalize": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "fkc_kmeans_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _int, _int]),
     "fkc_kmeans_lloyd": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp, _sz, _vp, _vp, _vp]),
+    "fkc_kmeans_lloyd_from": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp, _sz, _vp, _vp, _vp]),
     "fkc_quality_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "fkc_assigned_inertia": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, _vp, _sz, _vp]),
     "fkc_profile_enable": (None, [_int]),

@@ -83,12 +83,12 @@ def batch_kmeans_Euclid(
 
     if init_centroids is None:
         idx = torch.randint(0, N, (B, K), device=x.device)
-        centroids = torch.gather(x, dim=1, index=idx.unsqueeze(-1).expand(-1, -1, D))
+        init = torch.gather(x, dim=1, index=idx.unsqueeze(-1).expand(-1, -1, D))
     else:
-        centroids = init_centroids.contiguous().view(B, K, D).clone()
-    if centroids.dtype != x.dtype:
+        init = init_centroids.contiguous().view(B, K, D)
+    if init.dtype != x.dtype:
         raise RuntimeError("x and centroids must share dtype")
-    centroids = centroids.contiguous()
+    init = init.contiguous()
 
     cluster_ids = torch.empty((B, N), device=x.device, dtype=torch.int32)
 
@@ -97,8 +97,8 @@ def batch_kmeans_Euclid(
                 else torch.empty((B, N), device=x.device, dtype=torch.float32))
         sums_buf = torch.empty((B, K, D), device=x.device, dtype=torch.float32)
         counts_buf = torch.empty((B, K), device=x.device, dtype=torch.int32)
-        nxt = torch.empty_like(centroids)
-        cur = centroids
+        cur = init.clone()
+        nxt = torch.empty_like(cur)
         n_iters_run = 0
         for it in range(max_iters):
             new_c, shift, cluster_ids = _euclid_iter(
@@ -118,8 +118,11 @@ def batch_kmeans_Euclid(
             _lib.lib.fkc_kmeans_workspace_bytes(B, N, K, D, dt, max(max_iters, 1)),
             x.device)
         n_host = _lib.ctypes.c_int32(0)
-        _lib.check(_lib.lib.fkc_kmeans_lloyd(
-            x.data_ptr(), centroids.data_ptr(), cluster_ids.data_ptr(), B, N, K, D, dt,
-            int(max_iters), float(tol), ws.data_ptr(), ws.numel(), _lib.stream_of(x),
-            None, _lib.ctypes.byref(n_host)), "batch_kmeans_Euclid")
+        # The loop reads the initial centroids from `init` (never written) and
+        # updates `centroids`; the copy is fused into its first launch.
+        centroids = torch.empty_like(init)
+        _lib.check(_lib.lib.fkc_kmeans_lloyd_from(
+            x.data_ptr(), init.data_ptr(), centroids.data_ptr(), cluster_ids.data_ptr(),
+            B, N, K, D, dt, int(max_iters), float(tol), ws.data_ptr(), ws.numel(),
+            _lib.stream_of(x), None, _lib.ctypes.byref(n_host)), "batch_kmeans_Euclid")
     return cluster_ids, centroids, int(n_host.value)

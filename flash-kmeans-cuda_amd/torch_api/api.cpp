@@ -204,15 +204,18 @@ std::tuple<at::Tensor, at::Tensor, int64_t> batch_kmeans_euclid(
   const int64_t B = x.size(0), N = x.size(1), D = x.size(2), K = n_clusters;
   TORCH_CHECK(init_centroids.scalar_type() == x.scalar_type(),
               "x and centroids must share dtype");
-  at::Tensor cents = init_centroids.contiguous().view({B, K, D}).clone();
+  at::Tensor init = init_centroids.contiguous().view({B, K, D});
+  // The loop copies init into cents in its first launch; init is not written.
+  at::Tensor cents = at::empty_like(init);
   at::Tensor ids = at::empty({B, N}, at::TensorOptions().dtype(at::kInt).device(x.device()));
   const int dt = dtype_code(x);
   const int iters = static_cast<int>(max_iters);
   at::Tensor ws = workspace(fkc_kmeans_workspace_bytes(B, N, K, D, dt, iters > 0 ? iters : 1), x);
   int32_t n = 0;
-  check_rc(fkc_kmeans_lloyd(x.data_ptr(), cents.data_ptr(), ids.data_ptr<int32_t>(), B, N, K,
-                            D, dt, iters, static_cast<float>(tol), ws.data_ptr(), ws.numel(),
-                            stream_of(x), nullptr, &n),
+  check_rc(fkc_kmeans_lloyd_from(x.data_ptr(), init.data_ptr(), cents.data_ptr(),
+                                 ids.data_ptr<int32_t>(), B, N, K, D, dt, iters,
+                                 static_cast<float>(tol), ws.data_ptr(), ws.numel(),
+                                 stream_of(x), nullptr, &n),
            "batch_kmeans_euclid");
   return {ids, cents, static_cast<int64_t>(n)};
 }

@@ -200,6 +200,22 @@ FKC_CAPI int fkc_kmeans_lloyd(const void* x, void* centroids,
                               float tol, void* workspace,
                               size_t workspace_bytes, fkc_stream_t stream,
                               int32_t* n_iters_dev, int32_t* n_iters_host);
+/*
+ * fkc_kmeans_lloyd with the initial centroids read from init_centroids (left
+ * unmodified; it may be the same buffer as centroids) and the final ones
+ * written to centroids.  The copy is part of the loop's first launch, so a
+ * caller that keeps its initial centroids intact needs no separate copy
+ * (the reference's loop ping-pongs into init_centroids' storage,
+ * kmeans.py:157-193; this package's batch_kmeans_Euclid never writes it).
+ * Same workspace as fkc_kmeans_lloyd.
+ */
+FKC_CAPI int fkc_kmeans_lloyd_from(const void* x, const void* init_centroids,
+                                   void* centroids, int32_t* cluster_ids,
+                                   int64_t B, int64_t N, int64_t K, int64_t D,
+                                   int dtype, int max_iters, float tol,
+                                   void* workspace, size_t workspace_bytes,
+                                   fkc_stream_t stream, int32_t* n_iters_dev,
+                                   int32_t* n_iters_host);
 
 /*
  * Profiling hook for benchmarks (no counterpart in the reference): with

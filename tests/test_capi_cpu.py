@@ -77,6 +77,12 @@ def test_invalid_arguments_are_rejected_without_a_device():
     rc, msg = _err(L.fkc_kmeans_lloyd(fake, fake, fake, 1, 100, 4, 8, 1, -1, 0.0, None, 0,
                                       None, None, None))
     assert rc == 1
+    rc, msg = _err(L.fkc_kmeans_lloyd_from(fake, None, fake, fake, 1, 100, 4, 8, 1, 3, 0.0,
+                                           fake, 1 << 24, None, None, None))
+    assert rc == 1 and "null" in msg
+    rc, msg = _err(L.fkc_kmeans_lloyd_from(fake, fake, fake, fake, 1, 100, 4, 8, 1, 3, 0.0,
+                                           None, 0, None, None, None))
+    assert rc == 2 and "workspace" in msg
     rc, msg = _err(L.fkc_centroid_finalize(None, fake, fake, fake, 1, 4, 8, 1, None))
     assert rc == 1
     assert L.fkc_euclid_assign(fake, fake, None, fake, fake, 1 << 20, 10, 4, 16, 1, None) == 4

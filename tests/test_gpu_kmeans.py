@@ -283,6 +283,34 @@ def test_loop_with_sliced_assign(monkeypatch, B, N, K, dtype):
         assert torch.equal(a[0], r[0]) and torch.equal(a[1], r[1])
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_init_kept_and_entry_points_agree(dtype):
+    """batch_kmeans_Euclid never writes init_centroids (the copy is fused
+    into the loop's first launch); fkc_kmeans_lloyd (in place) and
+    fkc_kmeans_lloyd_from (init -> separate output) give the same bits; with
+    max_iters = 0 the returned centroids are the initial ones."""
+    from flash_kmeans_cuda import _lib, batch_kmeans_Euclid
+    B, N, K, D = 2, 5000, 300, 64
+    rng = np.random.default_rng(7)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    xt = _T(x, dtype)
+    init = xt[:, :K].clone()
+    keep = init.clone()
+    ids, cents, n = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=init)
+    assert torch.equal(init, keep) and n == 3
+    dt = _lib.dtype_code(xt.dtype)
+    ws = _lib.workspace(_lib.lib.fkc_kmeans_workspace_bytes(B, N, K, D, dt, 3), xt.device)
+    inplace = init.clone()
+    ids2 = torch.empty_like(ids)
+    _lib.check(_lib.lib.fkc_kmeans_lloyd(
+        xt.data_ptr(), inplace.data_ptr(), ids2.data_ptr(), B, N, K, D, dt, 3, 0.0,
+        ws.data_ptr(), ws.numel(), _lib.stream_of(xt), None, None), "lloyd")
+    torch.cuda.synchronize()
+    assert torch.equal(inplace, cents) and torch.equal(ids2, ids)
+    ids0, c0, n0 = batch_kmeans_Euclid(xt, K, max_iters=0, init_centroids=init)
+    assert n0 == 0 and torch.equal(c0, keep) and c0.data_ptr() != init.data_ptr()
+
+
 def test_deterministic_loop():
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c3"]
