@@ -311,6 +311,34 @@ def test_init_kept_and_entry_points_agree(dtype):
     assert n0 == 0 and torch.equal(c0, keep) and c0.data_ptr() != init.data_ptr()
 
 
+def test_large_k_three_sort_passes():
+    """1M points, K = 65536 (17-bit labels: three sort passes, 8-tile assign
+    on 2048 workgroups): invariants at a scale the oracle cannot run whole —
+    labels in range, every point counted once, the sort equal to torch's
+    stable sort, finite centroids — and a sampled label check against the
+    oracle with the returned centroids."""
+    from flash_kmeans_cuda import _C, batch_kmeans_Euclid
+    from flash_kmeans_cuda.ops import label_sort, row_sqnorm
+    B, N, K, D = 1, 1048576, 65536, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(B, N, D, device="cuda", generator=g).to(torch.float16)
+    ids, c, n = batch_kmeans_Euclid(x, K, max_iters=2, init_centroids=x[:, :K].clone())
+    assert n == 2 and int(ids.min()) >= 0 and int(ids.max()) < K
+    assert torch.isfinite(c.float()).all()
+    ids2 = _C.euclid_assign(x, c, row_sqnorm(x), row_sqnorm(c))
+    s, p = label_sort(ids2, K)
+    assert torch.equal(s[0].long(), torch.sort(ids2[0].long(), stable=True).values)
+    assert torch.equal(p[0].long(), torch.sort(ids2[0].long(), stable=True).indices)
+    assert int(torch.bincount(ids2[0].long(), minlength=K).sum()) == N
+    sub = np.random.default_rng(0).choice(N, 1024, replace=False)
+    xs = x[:, sub].cpu().numpy()
+    cs = c.cpu().numpy()
+    got = ids2[:, sub].cpu().numpy()
+    ref = O.assign(xs, cs, "f16")
+    nd, bad, worst = near_tie_report(xs, cs, "f16", got, ref)
+    assert bad == 0, f"{bad} non-near-tie disagreements (worst {worst:.3e})"
+
+
 def test_deterministic_loop():
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c3"]
