@@ -202,8 +202,8 @@ FKC_CAPI int fkc_kmeans_lloyd(const void* x, void* centroids,
                               int32_t* n_iters_dev, int32_t* n_iters_host);
 /*
  * fkc_kmeans_lloyd with the initial centroids read from init_centroids (left
- * unmodified; it may be the same buffer as centroids) and the final ones
- * written to centroids.  The copy is part of the loop's first launch, so a
+ * unmodified; it is either the same buffer as centroids or does not overlap
+ * it) and the final ones written to centroids.  The copy is part of the loop's first launch, so a
  * caller that keeps its initial centroids intact needs no separate copy
  * (the reference's loop ping-pongs into init_centroids' storage,
  * kmeans.py:157-193; this package's batch_kmeans_Euclid never writes it).
