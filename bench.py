@@ -28,6 +28,7 @@ Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--config c5]
                                        N-shards): assign TFLOPS,
                                        ms/iter (steady state and one-iteration
                                        call), roofline fraction ideal/measured
+       python bench.py --assign-sweep  euclid_assign alone over a list of shapes
        python bench.py --gemm-peak     hipBLASLt GEMM TFLOP/s (practical
                                        matrix-core ceiling on this part)
        python bench.py --traffic-probe / --lloyd-probe   workloads for
@@ -138,6 +139,57 @@ def _lloyd_probe(cfg) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": COPY_FLOATS * 4, "copy_bytes_written": COPY_FLOATS * 4,
                       "lloyd_calls": 4, "config": cfg.name}))
+    return 0
+
+
+SWEEP_SHAPES = [  # (B, N, K, D, dtype): the configs' neighbourhood and the routes
+    (1, 524288, 8192, 128, "f16"), (1, 524288, 8192, 128, "bf16"),
+    (1, 262144, 8192, 128, "f16"), (1, 1048576, 4096, 128, "f16"),
+    (1, 131072, 2048, 128, "f16"), (1, 131072, 16384, 128, "f16"),
+    (1, 65536, 8192, 128, "f16"), (1, 16384, 65536, 128, "f16"),
+    (1, 32768, 256, 128, "f16"), (1, 262144, 1024, 128, "f16"),
+    (8, 65536, 1024, 64, "bf16"), (1, 524288, 4096, 64, "f16"),
+    (1, 524288, 4096, 32, "f16"), (1, 262144, 2048, 256, "f16"),
+    (1, 262144, 2048, 96, "f16"), (4, 131072, 512, 128, "bf16"),
+    (1, 131072, 1024, 128, "f32"), (1, 100000, 300, 37, "f16"),
+]
+
+
+def _assign_sweep() -> int:
+    """euclid_assign alone over SWEEP_SHAPES (randn data, centroids drawn
+    from other randn rows): median of 5 x 10 launches with HIP events on the
+    current stream; one JSON line per shape with ms and TFLOP/s (2BNKD)."""
+    import statistics
+    import torch
+    from flash_kmeans_cuda import _C, _lib
+    from flash_kmeans_cuda.ops import row_sqnorm
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+    for (B, N, K, D, dn) in SWEEP_SHAPES:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        x = torch.randn(B, N, D, device="cuda", generator=g).to(dts[dn])
+        c = torch.randn(B, K, D, device="cuda", generator=g).to(dts[dn])
+        csq = row_sqnorm(c)
+        xsq = row_sqnorm(x)
+        ids = torch.empty((B, N), dtype=torch.int32, device="cuda")
+        for _ in range(3):
+            _C.euclid_assign(x, c, xsq, csq, ids)
+        ts = []
+        for _ in range(5):
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                _C.euclid_assign(x, c, xsq, csq, ids)
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) / 10)
+        ms = statistics.median(ts)
+        sliced = _lib.lib.fkc_euclid_assign_workspace_bytes(B, N, K, D, _lib.dtype_code(x.dtype)) > 0
+        print(json.dumps({"B": B, "N": N, "K": K, "D": D, "dtype": dn, "ms": round(ms, 5),
+                          "tflops": round(2.0 * B * N * K * D / ms / 1e9, 1),
+                          "k_sliced": bool(sliced)}), flush=True)
+        del x, c, csq, xsq, ids
     return 0
 
 
@@ -284,6 +336,8 @@ def main() -> int:
     ap.add_argument("--gemm-peak", action="store_true",
                     help="practical matrix-core ceiling: hipBLASLt GEMM TFLOP/s "
                          "(torch.matmul) on large fp16 / bf16 shapes")
+    ap.add_argument("--assign-sweep", action="store_true",
+                    help="euclid_assign alone over a fixed list of shapes (ms, TFLOP/s)")
     ap.add_argument("--report", nargs="?", const="c1,c2,c3,c4,c5,c5s8", default=None,
                     help="per-configuration table (comma-separated config names)")
     args = ap.parse_args()
@@ -302,6 +356,8 @@ def main() -> int:
         return _report(args.report.split(","))
     if args.gemm_peak:
         return _gemm_peak()
+    if args.assign_sweep:
+        return _assign_sweep()
     cfg = synth.CONFIGS[args.config]
     if args.traffic_probe:
         return _traffic_probe(cfg)

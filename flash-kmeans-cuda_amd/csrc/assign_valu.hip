@@ -46,7 +46,13 @@ assign_valu_kernel(const typename Elem<DT>::T* __restrict__ x,
   constexpr int PPW = VT / SPLIT;    // points per workgroup
   constexpr int KPL = VKC / SPLIT;   // centroids per lane per tile
   if (loop_done(ctrl)) return;
-  __shared__ float tile[VKC][VDC + 1];
+  // Rows padded to 36 floats: 16-byte aligned, so the lanes' reads of a
+  // row's features become 16-byte loads (one per four FMAs instead of one per
+  // FMA; 33-float rows forced 4-byte loads), with at most two-way bank
+  // conflicts when lanes read different rows (measured: (262144, 256, 128)
+  // fp32 1.00 -> 0.32 ms, (131072, 1024, 128) fp32 2.25 -> 1.92 ms,
+  // (100000, 300, 37) fp16 0.100 -> 0.082 ms).
+  __shared__ __attribute__((aligned(16))) float tile[VKC][VDC + 4];
   __shared__ float tile_q[VKC];
 
   const int tid = threadIdx.x;
