@@ -260,17 +260,24 @@ int launch_valu_split(const void* x, const void* c, const float* x_sq,
   return check_launch("assign_valu");
 }
 
-// Lanes per point: the smallest power of two (<= 16) that gives the grid at
-// least 1024 workgroups (4 per CU), so small N does not leave CUs idle.
+// Lanes per point: one while the grid has >= 512 workgroups (2 per CU),
+// else the smallest of 4, 8, 16 that gives >= 1024 workgroups.  Two lanes
+// per point were never the fastest (measured, ms at 1 / 2 / 4 / 8 / 16 lanes:
+// (131072, 1024, 128) fp32 0.94 / 1.93 / 1.05 / 1.05 / 1.63;
+// (65536, 1024, 64) fp32 0.43 / 0.53 / 0.27 / 0.29 / 0.43;
+// (32768, 512, 128) fp32 0.40 / 0.31 / 0.16 / 0.15 / 0.23;
+// (100000, 300, 37) fp16 0.18 / 0.11 / 0.088 / 0.10 / 0.15).
 template <int DT>
 int launch_valu_t(const void* x, const void* c, const float* x_sq,
                   const float* c_sq, int32_t* ids, int64_t B, int64_t N,
                   int64_t K, int64_t D, const int32_t* ctrl, hipStream_t s) {
   int split = 1;
-  while (split < 16 && B * ((N * split + VT - 1) / VT) < 1024) split <<= 1;
+  if (B * ((N + VT - 1) / VT) < 512) {
+    split = 4;
+    while (split < 16 && B * ((N * split + VT - 1) / VT) < 1024) split <<= 1;
+  }
   switch (split) {
     case 1: return launch_valu_split<DT, 1>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
-    case 2: return launch_valu_split<DT, 2>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
     case 4: return launch_valu_split<DT, 4>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
     case 8: return launch_valu_split<DT, 8>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);
     default: return launch_valu_split<DT, 16>(x, c, x_sq, c_sq, ids, B, N, K, D, ctrl, s);

@@ -206,6 +206,15 @@ def test_sliced_assign_workspace_errors(monkeypatch):
     assert _lib.lib.fkc_euclid_assign_workspace_bytes(1, 5000, 300, 128, 1) == 0
 
 
+@pytest.mark.parametrize("B,N,K,D,dtype", [(1, 140000, 40, 24, "f32"), (1, 140000, 33, 37, "f16")])
+def test_vector_route_one_lane_per_point(B, N, K, D, dtype):
+    """The VALU route with one lane per point (grids of >= 512 workgroups:
+    N >= 131072) against the oracle, fp32 and an odd fp16 width."""
+    x, c = _data(B, N, K, D, dtype, seed=N + D)
+    got = _gpu_assign(x, c, dtype)
+    _check(x, c, dtype, got, max_frac=1e-3)
+
+
 @pytest.mark.parametrize("B,N,K,D", [(1, 4096, 64, 128), (2, 1000, 33, 37), (1, 513, 300, 16)])
 def test_fp32_route_matches_oracle(B, N, K, D):
     x, c = _data(B, N, K, D, "f32", seed=N + D)
