@@ -341,7 +341,7 @@ SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
   // tile plus about 20 ns of look-back chain per tile, so fewer, larger
   // tiles win even when they leave CUs idle (measured at N = 524288,
   // K = 8192: 52 / 32 / 21 / 16 / 13.5 us per pass for 256 .. 4096-key
-  // tiles).  With at most 65536 keys in all the chain is short and smaller
+  // tiles; 8192-key tiles, 16 keys per thread, took 16.4 us).  With at most 65536 keys in all the chain is short and smaller
   // tiles shorten each tile's own work (1024 / 2048 / 4096-key tiles, us per
   // pass: 8.6 / 10.4 / 10.7 at B x N = 32768; 8.6 / 9.5 / 9.4 at 65536; but
   // 10.2 / 10.2 / 9.8 at 131072 and 12.0 / 10.4 / 9.6 at 8 x 65536).
