@@ -406,12 +406,21 @@ int lloyd_impl(const void* x, const void* init, void* centroids,
         (void)hipEventDestroy(e0);
         return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: profiling event creation failed");
       }
-      std::lock_guard<std::mutex> lock(g_prof.mu);
-      g_prof.starts.push_back(e0);
-      g_prof.stops.push_back(e1);
     }
     rc = launch_assign(x, centroids, L.x_sq, L.c_sq, cluster_ids, B, N, K, D,
                        dtype, ctrl, s, e0, e1, L.asg_ws, L.asg_ws_bytes);
+    // The events join the shared lists only once recorded, so another
+    // thread's fkc_profile_enable cannot destroy them before that.
+    if (e0 != nullptr) {
+      if (rc) {
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+      } else {
+        std::lock_guard<std::mutex> lock(g_prof.mu);
+        g_prof.starts.push_back(e0);
+        g_prof.stops.push_back(e1);
+      }
+    }
     if (!rc)
       rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
                              L.sort_ws, L.sort_ws_bytes, ctrl, s, it & 1);

@@ -44,8 +44,8 @@ def euclid_assign(x: torch.Tensor, centroids: torch.Tensor, x_sq: torch.Tensor,
     _require(x.dim() == 3 and centroids.dim() == 3,
              "x and centroids must be 3D (B,N,D)/(B,K,D)")
     _require(x.dtype == centroids.dtype, "x and centroids must share dtype")
-    _require(x_sq.dtype == torch.float32 and c_sq.dtype == torch.float32,
-             "x_sq and c_sq must be fp32")
+    _require((x_sq is None or x_sq.dtype == torch.float32)
+             and c_sq.dtype == torch.float32, "x_sq and c_sq must be fp32")
     B, N, D = x.shape
     K = centroids.shape[1]
     _require(centroids.shape[0] == B and centroids.shape[2] == D,

@@ -23,11 +23,13 @@ from .ops import centroid_finalize, centroid_update_sorted, euclid_assign, row_s
 
 def _assign_reads_x_sq(x: torch.Tensor) -> bool:
     """True when euclid_assign takes the fp32 route, which reads x_sq (the
-    counterpart of the reference's _can_skip_x_sq_for_assign, kmeans.py:48-70)."""
+    counterpart of the reference's _can_skip_x_sq_for_assign, kmeans.py:48-70).
+    Same rule as the library's route choice: the matrix-core route takes
+    fp16/bf16 with D a multiple of 8 up to 512."""
     import os
-    force = os.environ.get("FKC_ASSIGN_FORCE_SAFE", "").lower() in ("1", "true")
+    force = os.environ.get("FKC_ASSIGN_FORCE_SAFE", "") in ("1", "true")
     D = x.shape[-1]
-    mfma = x.dtype in (torch.float16, torch.bfloat16) and D % 16 == 0 and D <= 256
+    mfma = x.dtype in (torch.float16, torch.bfloat16) and D % 8 == 0 and 0 < D <= 512
     return force or not mfma
 
 
