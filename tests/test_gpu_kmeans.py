@@ -423,3 +423,60 @@ def test_lloyd_iteration_captures_into_a_graph():
         assert torch.equal(cents, e_c), f"replay {rep}: centroids"
         assert torch.equal(ids, e_i), f"replay {rep}: labels"
         state = e_c
+
+
+def test_two_threads_on_two_streams_with_profiling():
+    """The entry points keep no state across calls beyond the profiling
+    hook: two host threads run the Lloyd loop at once, each on its own
+    stream with its own workspace, while a third drains the profiling
+    events.  Each result equals the same call run alone, bit for bit, and the
+    hook counts every iteration's assign exactly once."""
+    import threading
+    import time
+    from flash_kmeans_cuda import _lib, batch_kmeans_Euclid
+    L = _lib.lib
+    rng = np.random.default_rng(11)
+    jobs = []
+    for (B, N, K, D, dtype) in [(1, 20000, 1100, 128, "f16"), (2, 8000, 300, 64, "bf16")]:
+        x = _T(O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype), dtype)
+        jobs.append((x, x[:, :K].clone(), K))
+    iters = 4
+    alone = [batch_kmeans_Euclid(x, K, max_iters=iters, init_centroids=c)
+             for (x, c, K) in jobs]
+    torch.cuda.synchronize()
+
+    L.fkc_profile_enable(1)
+    try:
+        out, errs = [None] * len(jobs), []
+
+        def run(i):
+            try:
+                x, c, K = jobs[i]
+                s = torch.cuda.Stream()
+                s.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(s):
+                    r = batch_kmeans_Euclid(x, K, max_iters=iters, init_centroids=c)
+                s.synchronize()
+                out[i] = r
+            except Exception as e:  # surfaced below
+                errs.append(e)
+
+        threads = [threading.Thread(target=run, args=(i,)) for i in range(len(jobs))]
+        for t in threads:
+            t.start()
+        tot = _lib.ctypes.c_double(0.0)
+        launches = _lib.ctypes.c_int64(0)
+        while any(t.is_alive() for t in threads):
+            _lib.check(L.fkc_profile_assign_ms(_lib.ctypes.byref(tot),
+                                               _lib.ctypes.byref(launches)), "profile")
+            time.sleep(0.001)
+        for t in threads:
+            t.join()
+        assert not errs, errs
+        _lib.check(L.fkc_profile_assign_ms(_lib.ctypes.byref(tot),
+                                           _lib.ctypes.byref(launches)), "profile")
+    finally:
+        L.fkc_profile_enable(0)
+    assert launches.value == iters * len(jobs) and tot.value > 0.0
+    for a, b in zip(alone, out):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and a[2] == b[2]
