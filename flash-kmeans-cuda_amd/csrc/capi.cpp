@@ -65,6 +65,14 @@ int sort_tile_override() {
   return (v == 256 || v == 512 || v == 1024 || v == 2048 || v == 4096) ? v : 0;
 }
 
+int sort_spin_override(int dflt) {
+  const char* s = std::getenv("FKC_SORT_SPIN");
+  if (!s || !*s) return dflt;
+  char* end = nullptr;
+  const long v = std::strtol(s, &end, 10);
+  return (*end == 0 && v >= 0 && v <= dflt) ? (int)v : dflt;
+}
+
 // ------------------------------------------------------------- profiling
 namespace {
 // Process-wide profiling state.  The loop reads `period` without a lock;
@@ -323,6 +331,34 @@ int fkc_assigned_inertia(const void* x, const void* centroids,
   return launch_quality(x, centroids, cluster_ids, B, N, K, D, dtype, inertia,
                         empty_clusters, workspace, workspace_bytes,
                         reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t fkc_sampled_inertia_workspace_bytes(int64_t B, int64_t S, int64_t K,
+                                           int64_t D, int dtype) {
+  if (B <= 0 || S <= 0 || K < 1 || D < 1 || dtype_ok(dtype, "sampled_inertia"))
+    return 0;
+  return sample_workspace_bytes(B, S, K, D, dtype);
+}
+
+int fkc_sampled_inertia(const void* x, const void* centroids,
+                        const int32_t* sample_idx, int64_t S, int64_t B,
+                        int64_t N, int64_t K, int64_t D, int dtype,
+                        double* inertia, void* workspace,
+                        size_t workspace_bytes, fkc_stream_t stream) {
+  g_err[0] = 0;
+  if (int rc = shape_ok(B, N, K, D, "sampled_inertia")) return rc;
+  if (int rc = dtype_ok(dtype, "sampled_inertia")) return rc;
+  if (S < 0 || S > INT32_MAX - 65536)
+    return fail(FKC_ERR_INVALID, "sampled_inertia: bad sample count %lld",
+                (long long)S);
+  if (B == 0) return FKC_OK;
+  if (!inertia) return fail(FKC_ERR_INVALID, "sampled_inertia: null inertia");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (S == 0 || N == 0) return launch_fill_f64(inertia, 0.0, B, s);
+  if (!x || !centroids || !sample_idx)
+    return fail(FKC_ERR_INVALID, "sampled_inertia: null pointer argument");
+  return launch_sampled_inertia(x, centroids, sample_idx, S, B, N, K, D, dtype,
+                                inertia, workspace, workspace_bytes, s);
 }
 
 size_t fkc_kmeans_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,

@@ -73,6 +73,12 @@ __global__ void fill_f32_kernel(float* p, float v, int64_t n) {
   for (int64_t j = i; j < n; j += stride) p[j] = v;
 }
 
+__global__ void fill_f64_kernel(double* p, double v, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t j = i; j < n; j += stride) p[j] = v;
+}
+
 __global__ void iota_i32_kernel(int32_t* p, int64_t B, int64_t N) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -214,6 +220,13 @@ int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s) {
   hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, v,
                      n);
   return check_launch("fill_f32");
+}
+
+int launch_fill_f64(double* p, double v, int64_t n, hipStream_t s) {
+  if (n <= 0) return FKC_OK;
+  hipLaunchKernelGGL(fill_f64_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, v,
+                     n);
+  return check_launch("fill_f64");
 }
 
 int launch_iota_i32(int32_t* p, int64_t B, int64_t N, hipStream_t s) {

@@ -83,6 +83,9 @@ void label_sort_reset_region(void* ws, int64_t B, int64_t N, int64_t K,
                              int32_t** p, int64_t* n);
 // FKC_SORT_TILE=256|512|1024|2048|4096: keys per sort tile; 0 = auto.
 int sort_tile_override();
+// FKC_SORT_SPIN=n (n >= 0, tests): look-back spin budget of the sort's tile
+// walks instead of dflt; 0 sends every tile after the first to the recount.
+int sort_spin_override(int dflt);
 
 // ---------------------------------------------------------------- update
 size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D);
@@ -134,6 +137,7 @@ int launch_lloyd_prologue(const void* init, void* cent, float* c_sq,
 // p[b*N + n] = n for every batch row b.
 int launch_iota_i32(int32_t* p, int64_t B, int64_t N, hipStream_t s);
 int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);
+int launch_fill_f64(double* p, double v, int64_t n, hipStream_t s);
 int launch_converge_check(const float* shift, int it, float tol, int32_t* ctrl,
                           hipStream_t s);
 
@@ -141,11 +145,22 @@ int launch_converge_check(const float* shift, int it, float tol, int32_t* ctrl,
 bool force_safe_assign();
 // ---------------------------------------------------------------- quality
 size_t quality_workspace_bytes(int64_t B, int64_t N, int64_t K);
-// inertia (B doubles) and empty (B ints) are device pointers, either NULL.
+// inertia (B doubles) and empty (one int: k empty in every row) are device
+// pointers, either NULL.  sidx (optional, N entries shared by every row):
+// the rows are samples x[:, sidx]; a row whose index is outside [0, sN)
+// adds nothing.
 int launch_quality(const void* x, const void* c, const int32_t* ids,
                    int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
                    double* inertia, int32_t* empty, void* ws, size_t ws_bytes,
-                   hipStream_t s);
+                   hipStream_t s, const int32_t* sidx = nullptr,
+                   int64_t sN = 0);
+// Nearest-centroid inertia of the S sampled points idx[0..S) of every row.
+size_t sample_workspace_bytes(int64_t B, int64_t S, int64_t K, int64_t D,
+                              int dtype);
+int launch_sampled_inertia(const void* x, const void* c, const int32_t* idx,
+                           int64_t S, int64_t B, int64_t N, int64_t K,
+                           int64_t D, int dtype, double* inertia, void* ws,
+                           size_t ws_bytes, hipStream_t s);
 
 // FKC_NTILES=1|2|4|8: 16-point tiles per wave in the MFMA kernel; 0 = auto.
 int ntiles_override();

@@ -30,8 +30,14 @@
 // A status word is 64 bits: flag in bits 63..62 (published count, or
 // inclusive prefix), count in the rest, read and written with relaxed
 // agent-scope atomics, so a reader sees flag and count together and no fence
-// is needed.  Each wait is bounded: past the spin limit the tile records an
-// error in the workspace and proceeds, so every workgroup always exits.
+// is needed.  Each wait is bounded: a digit whose walk runs past the spin
+// limit stops waiting, and the workgroup counts that digit's keys in every
+// earlier tile straight from the pass's input (written by the previous
+// launch, so always complete).  That gives the same exclusive prefix as the
+// walk, so the output is correct either way and every workgroup exits; the
+// workspace's first word counts how often the recount ran (zero in a normal
+// run: every tile a walk waits for took its tile index earlier and is
+// already running).
 //
 // The global digit counts accumulate into one of two buffers (the call's
 // phase); the upsweep clears the other, so a caller that alternates phases
@@ -50,7 +56,7 @@ constexpr int UPT = 512;          // threads of the upsweep kernel
 constexpr uint64_t ST_AGG = 1ull << 62;  // the tile's own digit count
 constexpr uint64_t ST_INC = 2ull << 62;  // inclusive prefix over tiles 0..t
 constexpr uint64_t ST_VAL = (1ull << 62) - 1;
-constexpr int SPIN_LIMIT = 1 << 18;  // empty polls per thread and pass (< 1 s)
+constexpr int SPIN_LIMIT = 1 << 18;  // empty polls per digit walk (< 1 s)
 
 struct PassDesc {
   int passes;
@@ -75,7 +81,7 @@ __device__ inline uint32_t sort_key(int32_t id, int K) {
 
 // Workspace layout, shared by the size query and the launcher.
 struct SortBufs {
-  int32_t* err;      // [1] look-back spin limit reached (never in a good run)
+  int32_t* err;      // [1] recounts after a look-back wait ran out of spins
   int32_t* gcnt;     // [2 phases][B][MAXP][256] global digit counts; err and
                      // phase 0 are contiguous (one fill clears both)
   int32_t* tctr;     // [B][MAXP] tile counters
@@ -188,7 +194,8 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
                      uint64_t* __restrict__ status,     // this pass, row stride slen
                      int64_t slen, int32_t* __restrict__ tctr,  // this pass, row stride MAXP
                      int32_t* __restrict__ err, int N, int K, int shift,
-                     int bits, const int32_t* __restrict__ ctrl) {
+                     int bits, int spin_limit,
+                     const int32_t* __restrict__ ctrl) {
   constexpr int SW = Geom<TILE>::SW;
   constexpr int PER_WAVE = Geom<TILE>::PER_WAVE;
   constexpr int CHUNKS = Geom<TILE>::CHUNKS;
@@ -198,6 +205,7 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
   __shared__ int dstart[256];
   __shared__ int wtot[8];
   __shared__ int s_tile;
+  __shared__ int s_recount;  // a digit of this tile stopped waiting
   __shared__ int32_t skey[TILE];
   __shared__ int32_t sval[TILE];
   const int nb = 1 << bits;
@@ -207,7 +215,10 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
   // in flight together with the tile-counter atomic.
   const int gc = tid < nb ? gcnt[(size_t)b * MAXP * 256 + tid] : 0;
   for (int i = tid; i < SW * 256; i += ST) (&cnt[0][0])[i] = 0;
-  if (tid == 0) s_tile = atomicAdd(&tctr[(size_t)b * MAXP], 1);
+  if (tid == 0) {
+    s_tile = atomicAdd(&tctr[(size_t)b * MAXP], 1);
+    s_recount = 0;
+  }
   __syncthreads();
   const int tile = s_tile;
 
@@ -261,6 +272,7 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
   }
   // Tile-local and global exclusive digit prefixes.
   const int2 pre = scan256x2(total, gc, wtot, tid);
+  bool stopped = false;  // this digit's walk ran out of spins
   if (tid < nb) {
     int64_t excl = 0;
     if (tile > 0) {
@@ -268,28 +280,52 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
       int spins = 0;  // one budget for the whole walk
       for (int t = tile - 1;; --t) {
         uint64_t v = 0;
-        for (;; ++spins) {
+        for (;;) {
+          if (spins >= spin_limit) {
+            stopped = true;
+            break;
+          }
           v = __hip_atomic_load(col + (size_t)t * 256, __ATOMIC_RELAXED,
                                 __HIP_MEMORY_SCOPE_AGENT);
           if (v & (ST_AGG | ST_INC)) break;
-          if (spins >= SPIN_LIMIT) {
-            atomicOr(err, 1);
-            v = ST_INC;
-            break;
-          }
+          ++spins;
           __builtin_amdgcn_s_sleep(1);
         }
+        if (stopped) break;
         excl += (int64_t)(v & ST_VAL);
         if ((v & ST_INC) || t == 0) break;
       }
-      __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
-                         ST_INC | (uint64_t)(excl + total), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      if (stopped)
+        s_recount = 1;
+      else
+        __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
+                           ST_INC | (uint64_t)(excl + total), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
     dstart[tid] = pre.x;
     gbase[tid] = pre.y + (int)excl - pre.x;
   }
   __syncthreads();
+  if (s_recount) {  // workgroup-uniform; never taken in a normal run
+    // Count the digits of keys 0 .. tbase-1 of this pass's input (the
+    // earlier tiles) in LDS; a stopped digit's exclusive prefix is its
+    // count.  skey is free until the placement below.
+    int* rc = skey;
+    for (int i = tid; i < 256; i += ST) rc[i] = 0;
+    __syncthreads();
+    for (int n = tid; n < tbase; n += ST)
+      atomicAdd(&rc[(sort_key(kb[n], K) >> shift) & dmask], 1);
+    __syncthreads();
+    if (stopped) {
+      const int excl = rc[tid];
+      __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
+                         ST_INC | (uint64_t)(excl + total), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      gbase[tid] = pre.y + excl - pre.x;
+    }
+    if (tid == 0) atomicAdd(err, 1);
+    __syncthreads();
+  }
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     if (rank[c] >= 0) {
@@ -315,10 +351,10 @@ void launch_onesweep(dim3 grid, hipStream_t s, const int32_t* kin,
                      const int32_t* vin, int32_t* kout, int32_t* vout,
                      const int32_t* gcnt, uint64_t* status, int64_t slen,
                      int32_t* tctr, int32_t* err, int N, int K, int shift,
-                     int bits, const int32_t* ctrl) {
+                     int bits, int spin_limit, const int32_t* ctrl) {
   hipLaunchKernelGGL((sort_onesweep_kernel<TILE>), grid, dim3(Geom<TILE>::ST),
                      0, s, kin, vin, kout, vout, gcnt, status, slen, tctr, err,
-                     N, K, shift, bits, ctrl);
+                     N, K, shift, bits, spin_limit, ctrl);
 }
 
 }  // namespace
@@ -401,6 +437,9 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
   int rc = check_launch("sort_upsweep");
   if (rc) return rc;
 
+  // FKC_SORT_SPIN (tests): a smaller look-back spin budget; 0 makes every
+  // tile after the first take the recount path.
+  const int spin = sort_spin_override(SPIN_LIMIT);
   const int32_t* kin = ids;
   const int32_t* vin = nullptr;  // identity payload on the first pass
   for (int i = 0; i < p.passes; ++i) {
@@ -414,23 +453,23 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
     switch (p.tile) {
       case 256:
         launch_onesweep<256>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
         break;
       case 512:
         launch_onesweep<512>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
         break;
       case 1024:
         launch_onesweep<1024>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
         break;
       case 2048:
         launch_onesweep<2048>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
         break;
       default:
         launch_onesweep<4096>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], ctrl);
+                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
         break;
     }
     rc = check_launch("sort_onesweep");

@@ -33,10 +33,15 @@
 //                  over L units adds at most 127 + L/64 partial rows, 32 rows
 //                  in flight per wave (four lane groups, eight rows each).
 //
-// Mode "add" (the _C / C-ABI contract) adds into caller-zeroed outputs;
-// mode "overwrite" (the Lloyd loop, where every label is valid) stores, and
-// the run start of each label also zeroes the empty bins below it, so no
-// separate clearing pass is needed.
+// Mode "add" (the _C / C-ABI contract) adds into caller-zeroed outputs with
+// atomic adds, so it is correct for labels in any order, as the reference's
+// atomics are: a label whose rows are not contiguous (unsorted input, or
+// invalid labels between its rows) forms several runs that each add their
+// share.  With sorted input every bin still gets exactly one add, so the
+// result is the same bits on every run.  Mode "overwrite" (the Lloyd loop,
+// where every label is valid and sorted) stores, and the run start of each
+// label also zeroes the empty bins below it, so no separate clearing pass is
+// needed.
 #include "device_util.hpp"
 #include "fkc_internal.hpp"
 
@@ -318,14 +323,14 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
             if (overwrite)
               dst[col[i] + v] = a[i][v];
             else
-              dst[col[i] + v] += a[i][v];
+              unsafeAtomicAdd(dst + col[i] + v, a[i][v]);
           }
         }
       if (lead && lane == 0) {
         if (overwrite)
           cntb[id] = e - s;
         else
-          cntb[id] += e - s;
+          atomicAdd(cntb + id, e - s);
       }
     }
   };
@@ -494,7 +499,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
 // in increasing i (eight loads in flight per lane before their adds) over
 // V-wide column vectors, then the group sums are added in group order.  The
 // bracketing depends only on n, so the result is reproducible bit for bit.
-// Mode 0 stores out, mode 1 adds into it.
+// Mode 0 stores out, mode 1 adds into it atomically.
 template <int V>
 __device__ inline void ld_cols(const float* p, float* o) {
   if constexpr (V == 4) {
@@ -546,7 +551,12 @@ __device__ inline void wave_ordered_sum(const float* first, int n, int D,
       for (int v = 0; v < V; ++v) tot[v] += __shfl(acc[v], gg * LG + sub, 64);
     if (g == 0 && cok) {
 #pragma unroll
-      for (int v = 0; v < V; ++v) out[c + v] = add ? out[c + v] + tot[v] : tot[v];
+      for (int v = 0; v < V; ++v) {
+        if (add)
+          unsafeAtomicAdd(out + c + v, tot[v]);
+        else
+          out[c + v] = tot[v];
+      }
     }
   }
 }
@@ -697,7 +707,7 @@ update_merge_kernel(const float* __restrict__ part,
     if (overwrite)
       *cp = len;
     else
-      *cp += len;
+      atomicAdd(cp, len);
   }
 }
 

@@ -21,18 +21,6 @@ from . import _lib
 from .ops import centroid_finalize, centroid_update_sorted, euclid_assign, row_sqnorm
 
 
-def _assign_reads_x_sq(x: torch.Tensor) -> bool:
-    """True when euclid_assign takes the fp32 route, which reads x_sq (the
-    counterpart of the reference's _can_skip_x_sq_for_assign, kmeans.py:48-70).
-    Same rule as the library's route choice: the matrix-core route takes
-    fp16/bf16 with D a multiple of 8 up to 512."""
-    import os
-    force = os.environ.get("FKC_ASSIGN_FORCE_SAFE", "") in ("1", "true")
-    D = x.shape[-1]
-    mfma = x.dtype in (torch.float16, torch.bfloat16) and D % 8 == 0 and 0 < D <= 512
-    return force or not mfma
-
-
 def _euclid_iter(x, x_sq, centroids, *, compute_shift=True, cluster_ids_buf=None,
                  sums_buf=None, counts_buf=None, new_centroids_buf=None):
     """One assign+update+finalize step (kmeans.py:73-105).
@@ -95,8 +83,11 @@ def batch_kmeans_Euclid(
     cluster_ids = torch.empty((B, N), device=x.device, dtype=torch.int32)
 
     if verbose:
-        x_sq = (row_sqnorm(x) if _assign_reads_x_sq(x)
-                else torch.empty((B, N), device=x.device, dtype=torch.float32))
+        # The reference skips x_sq where its raw-distance route ignores it
+        # (kmeans.py:23-70,146-151); which route the library takes is its own
+        # decision, so this debug path always passes real norms (one pass
+        # over x per call).  The native loop needs no x_sq from the caller.
+        x_sq = row_sqnorm(x)
         sums_buf = torch.empty((B, K, D), device=x.device, dtype=torch.float32)
         counts_buf = torch.empty((B, K), device=x.device, dtype=torch.int32)
         cur = init.clone()

@@ -70,8 +70,10 @@ def label_sort(cluster_ids: torch.Tensor, K: int, *,
 
     Labels outside [0, K) sort after every valid label, in index order.
     workspace: optional caller-owned uint8 CUDA tensor of at least
-    fkc_label_sort_workspace_bytes(B, N, K) bytes, 256-byte aligned; its first
-    int32 is the sort's health word (nonzero after the call: invalid output).
+    fkc_label_sort_workspace_bytes(B, N, K) bytes, 256-byte aligned; after
+    the call its first int32 counts the tiles whose bounded look-back wait ran
+    out and that recounted their prefix instead (a diagnostic: the output is
+    valid either way).
     """
     cluster_ids = _ensure_contig(cluster_ids, "cluster_ids")
     if cluster_ids.dtype != torch.int32:

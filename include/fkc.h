@@ -23,7 +23,7 @@
  *   flash_kmeans_cuda/csrc/bindings.cpp:107-127        (_C extension module)
  *   flash_kmeans_cuda/kmeans.py:108-195                (Lloyd driver loop)
  *   flash_kmeans_cuda/ops.py:58-112                    (torch.sort call site)
- *   benchmarks/quality_compare.py:69-90                (inertia evaluator)
+ *   benchmarks/quality_compare.py:69-116               (quality evaluator)
  */
 #ifndef FKC_H_
 #define FKC_H_
@@ -114,10 +114,11 @@ FKC_CAPI int fkc_row_sqnorm(const void* src, float* out, int64_t rows,
  * order.  Labels outside [0,K) sort after every valid label, in index order.
  * Replaces torch.sort(cluster_ids, dim=1) at ops.py:89 (the reference asks
  * stable=False; this sort is always stable).
- * The workspace's first int32 is the sort's health word, cleared by every
- * call: nonzero after the call completes means a workgroup of a pass gave up
- * waiting for its predecessors' tile counts (a bounded wait that never
- * expires in a correct run) and the output is not valid.
+ * The output is always valid.  Each pass chains its key tiles with bounded
+ * waits (decoupled look-back); a tile whose wait runs out recounts its
+ * prefix from the pass's input instead, which gives the same result.  The
+ * workspace's first int32, cleared by every call, counts those recounts
+ * (0 in a normal run; a diagnostic, not an error).
  */
 FKC_CAPI size_t fkc_label_sort_workspace_bytes(int64_t B, int64_t N,
                                                int64_t K);
@@ -130,9 +131,12 @@ FKC_CAPI int fkc_label_sort(const int32_t* cluster_ids, int32_t* sorted_ids,
  * Centroid accumulation over label-sorted rows.  Adds into sums/counts
  * (the caller zeroes them first, as _C.centroid_update_sorted expects,
  * bindings.cpp:73-90); labels outside [0,K) are skipped
- * (update_sorted.cu:95,167).  ids_sorted must be non-decreasing over the
- * valid labels of each batch row.  Summation is fp32, in sorted order within
- * a run, and deterministic: the same inputs give the same bits.
+ * (update_sorted.cu:95,167).  Each maximal run of equal consecutive labels
+ * adds its fp32 row sum (rows in sorted order) and its length with atomic
+ * adds (update_sorted.cu:105,109), so any label order gives the right
+ * totals.  When the rows of each valid label are contiguous (sorted labels,
+ * invalid ones anywhere outside those runs) every bin gets exactly one add
+ * and the result is deterministic: the same inputs give the same bits.
  * _sorted reads x_sorted row p for sorted position p (update_sorted.cu:39-116);
  * _indexed reads x row sorted_idx[p] (update_sorted.cu:118-186).
  */
@@ -164,10 +168,13 @@ FKC_CAPI int fkc_centroid_finalize(const float* sums, const int32_t* counts,
  * reference's benchmarks/quality_compare.py:69-90, `_assigned_inertia` and
  * `_empty_clusters`):
  *   inertia[b] = sum_n sum_d (float(x[b,n,d]) - float(c[b,ids[b,n],d]))^2,
- *                difference and square in fp32, sum in fp64;
- *   empty_clusters[b] = number of k in [0,K) that no point of row b carries.
+ *                difference and square in fp32, sum in fp64 (the reference
+ *                returns the sum over b);
+ *   *empty_clusters = number of k in [0,K) that no point of any batch row
+ *                carries (the reference counts the flattened labels into one
+ *                K-bin histogram, `bincount(ids.reshape(-1)) == 0`).
  * Rows labelled outside [0,K) add nothing and are not counted.  inertia (B
- * doubles) and empty_clusters (B int32) are device pointers; either may be
+ * doubles) and empty_clusters (one int32) are device pointers; either may be
  * NULL (x and centroids may then be NULL too when inertia is).  The result
  * is bitwise reproducible (fixed summation order).
  */
@@ -178,6 +185,26 @@ FKC_CAPI int fkc_assigned_inertia(const void* x, const void* centroids,
                                   double* inertia, int32_t* empty_clusters,
                                   void* workspace, size_t workspace_bytes,
                                   fkc_stream_t stream);
+
+/*
+ * Inertia of a point sample (`_sample_exact_inertia`,
+ * benchmarks/quality_compare.py:91-116): inertia[b] = sum over the S indices
+ * n = sample_idx[s] (device int32, the same indices in every batch row) of
+ * the squared distance from x[b,n] to its nearest centroid of row b.  The
+ * nearest centroid is the assignment's (fkc_euclid_assign) and the distance
+ * is summed as in fkc_assigned_inertia (fp32 differences and squares, fp64
+ * total); the reference forms x_sq + c_sq - 2<x,c> in fp32 and takes its
+ * minimum, clamped at 0, which agrees up to fp32 rounding.  An index outside
+ * [0,N) adds nothing.  inertia: B device doubles.
+ */
+FKC_CAPI size_t fkc_sampled_inertia_workspace_bytes(int64_t B, int64_t S,
+                                                    int64_t K, int64_t D,
+                                                    int dtype);
+FKC_CAPI int fkc_sampled_inertia(const void* x, const void* centroids,
+                                 const int32_t* sample_idx, int64_t S,
+                                 int64_t B, int64_t N, int64_t K, int64_t D,
+                                 int dtype, double* inertia, void* workspace,
+                                 size_t workspace_bytes, fkc_stream_t stream);
 
 /*
  * Whole Lloyd loop of batch_kmeans_Euclid (kmeans.py:108-195) in one call.

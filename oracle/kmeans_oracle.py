@@ -15,8 +15,9 @@ Reference (OpsiClear/flash-kmeans-cuda) semantics restated here:
               (runs of equal sorted labels; labels outside [0,K) skipped)
   finalize    ops.py:115-130, csrc/update/update_finalize.cu:39-66
   loop        flash_kmeans_cuda/kmeans.py:73-195
-  quality     benchmarks/quality_compare.py:69-90 (assigned inertia with
-              fp32 differences and squares summed in fp64; empty clusters)
+  quality     benchmarks/quality_compare.py:69-116 (assigned inertia with
+              fp32 differences and squares summed in fp64; empty clusters
+              over the flattened labels; sampled nearest-centroid inertia)
 
 Arithmetic choices (documented, not the reference's exact rounding):
   * assign ranks exact squared distances: x_sq + c_sq - 2<x,c> evaluated in
@@ -194,9 +195,17 @@ def finalize(sums: np.ndarray, counts: np.ndarray, old: np.ndarray, dtype: str) 
 
 
 def shift(new: np.ndarray, old: np.ndarray, dtype: str) -> float:
-    """max over (b,k) of ||new - old||_2 (kmeans.py:104)."""
-    d = to_f64(new, dtype) - to_f64(old, dtype)
-    return float(np.sqrt((d * d).sum(-1)).max()) if d.size else 0.0
+    """max over every (b,k) of ||new - old||_2, in float32 as the reference
+    computes it: `(new.float() - old.float()).norm(dim=-1).max()`
+    (kmeans.py:104), the loop stopping once it is < tol (kmeans.py:190).
+    The difference, squares, row sums and square root are float32 (numpy's
+    pairwise float32 sum; the reference's reduction order differs by a few
+    ulp at most)."""
+    d = to_f32(new, dtype) - to_f32(old, dtype)
+    if d.size == 0:
+        return 0.0
+    sq = np.sum(d * d, axis=-1, dtype=np.float32)
+    return float(np.sqrt(sq).max())
 
 
 # ----------------------------------------------------------------- loop
@@ -251,12 +260,35 @@ def assigned_inertia(x: np.ndarray, ids: np.ndarray, c: np.ndarray, dtype: str) 
     return out
 
 
-def empty_clusters(ids: np.ndarray, K: int) -> np.ndarray:
-    """Per batch row: number of k in [0,K) that no point carries
-    (quality_compare.py:86-88, bincount == 0)."""
-    out = []
-    for b in range(ids.shape[0]):
-        ib = np.asarray(ids[b]).astype(np.int64)
-        ib = ib[(ib >= 0) & (ib < K)]
-        out.append(int((np.bincount(ib, minlength=K) == 0).sum()))
-    return np.asarray(out, dtype=np.int64)
+def empty_clusters(ids: np.ndarray, K: int) -> int:
+    """Number of k in [0,K) that no point of any batch row carries: the
+    labels of all rows are counted into one histogram of K bins
+    (quality_compare.py:86-88, `bincount(ids.reshape(-1), minlength=K) == 0`),
+    so at B > 1 a k is empty only when every row leaves it empty.  Labels
+    outside [0,K) are ignored (the reference's bincount rejects negative
+    labels and grows extra bins past K-1)."""
+    flat = np.asarray(ids).astype(np.int64).reshape(-1)
+    flat = flat[(flat >= 0) & (flat < K)]
+    return int((np.bincount(flat, minlength=K) == 0).sum())
+
+
+def sample_exact_inertia(x: np.ndarray, c: np.ndarray, sample_idx: np.ndarray,
+                         dtype: str) -> float:
+    """Inertia of a point sample against the nearest centroid, over every
+    batch row (quality_compare.py:91-116, `_sample_exact_inertia`): for each
+    sampled index n (the same indices in every row) the distance
+    x_sq + c_sq - 2<x,c> is formed in float32 from float32 products, its
+    minimum over k is clamped at 0, and the minima are summed in float64.
+    The reference draws sample_idx with torch.randperm on the device; here it
+    is an argument."""
+    xs = to_f32(np.asarray(x)[:, np.asarray(sample_idx, dtype=np.int64)], dtype)
+    cf = to_f32(c, dtype)
+    total = 0.0
+    for b in range(xs.shape[0]):
+        x_sq = np.sum(xs[b] * xs[b], axis=-1, dtype=np.float32)
+        c_sq = np.sum(cf[b] * cf[b], axis=-1, dtype=np.float32)
+        cross = (xs[b] @ cf[b].T).astype(np.float32)
+        dist = (x_sq[:, None] + c_sq[None, :]) - np.float32(2.0) * cross
+        total += float(np.maximum(dist.min(axis=-1), np.float32(0.0))
+                       .astype(np.float64).sum())
+    return total

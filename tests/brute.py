@@ -106,6 +106,22 @@ def assigned_inertia(x_rows, ids, cents, K):
     return tot
 
 
-def empty_clusters(ids, K):
-    seen = set(k for k in ids if 0 <= k < K)
+def empty_clusters(rows_of_ids, K):
+    """rows_of_ids: one list of labels per batch row.  A k in [0,K) is empty
+    when no row carries it (the rows' labels share one set of K bins)."""
+    seen = set(k for ids in rows_of_ids for k in ids if 0 <= k < K)
     return sum(1 for k in range(K) if k not in seen)
+
+
+def nearest_sqdist(p, cents):
+    """Exact minimum over centroids of the squared distance (Python floats)."""
+    return min(math.fsum((a - b) * (a - b) for a, b in zip(p, q)) for q in cents)
+
+
+def max_row_norm(new_rows, old_rows):
+    """max over rows of the Euclidean norm of new - old (exact sum, Python
+    floats)."""
+    best = 0.0
+    for n, o in zip(new_rows, old_rows):
+        best = max(best, math.sqrt(math.fsum((a - b) * (a - b) for a, b in zip(n, o))))
+    return best

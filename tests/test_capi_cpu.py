@@ -221,3 +221,29 @@ def test_synth_generators_are_deterministic():
     assert not np.array_equal(a[0], a[1])  # per-batch seeds
     p = synth.zipf_probs(8192, 1.1)
     assert abs(p.sum() - 1) < 1e-12 and 0.14 < p[0] < 0.16
+
+
+def test_sampled_inertia_validation_without_a_device():
+    """fkc_sampled_inertia (quality_compare.py:91-116 counterpart): argument
+    checks come before any device work."""
+    from flash_kmeans_cuda import _lib
+    L = _lib.lib
+    assert "fkc_sampled_inertia" in _declared()
+    fake = 0x1000
+    rc, msg = _err(L.fkc_sampled_inertia(fake, fake, fake, 4, 1, 10, 0, 16, 1, fake,
+                                         fake, 1 << 20, None))
+    assert rc == 1 and "K>=1" in msg
+    rc, msg = _err(L.fkc_sampled_inertia(fake, fake, fake, -1, 1, 10, 4, 16, 1, fake,
+                                         fake, 1 << 20, None))
+    assert rc == 1 and "sample count" in msg
+    rc, msg = _err(L.fkc_sampled_inertia(fake, fake, None, 4, 1, 10, 4, 16, 1, fake,
+                                         fake, 1 << 20, None))
+    assert rc == 1 and "null" in msg
+    rc, msg = _err(L.fkc_sampled_inertia(fake, fake, fake, 4, 1, 10, 4, 16, 1, None,
+                                         fake, 1 << 20, None))
+    assert rc == 1 and "null inertia" in msg
+    need = L.fkc_sampled_inertia_workspace_bytes(2, 100, 7, 40, 2)
+    # sampled rows (bf16), their norms, c_sq, labels and the evaluator's partials
+    assert need >= 2 * 100 * 40 * 2 + 2 * 100 * 4 + 2 * 7 * 4 + 2 * 100 * 4 + 7 * 4
+    assert L.fkc_sampled_inertia_workspace_bytes(0, 100, 7, 40, 2) == 0
+    assert L.fkc_sampled_inertia(None, None, None, 0, 0, 0, 4, 8, 1, None, None, 0, None) == 0

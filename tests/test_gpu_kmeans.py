@@ -176,19 +176,51 @@ def test_dtypes_contract(dtype):
     assert u.unique().numel() > 16
 
 
-def test_tol_stops_early_and_matches_truncated_run():
+def _oracle_shifts(x, init, K, dtype, iters):
+    """The oracle's shift (kmeans.py:104) of every iteration of a tol = 0 run."""
+    cur, out = init.copy(), []
+    for _ in range(iters):
+        new = O.lloyd_step(x, cur, K, dtype)[0]
+        out.append(O.shift(new, cur, dtype))
+        cur = new
+    return out
+
+
+def test_tol_stops_at_the_oracles_iteration():
+    """c4's batched bf16 loop with a tolerance (kmeans.py:104,190): tol is
+    put between the first nonzero oracle shift that is at least 2x below
+    every earlier one and the smallest earlier one, so the GPU loop must stop
+    after exactly the oracle's iteration; the result equals a tol = 0 run of
+    that many iterations bit for bit, and init is not modified."""
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c4"]
     x, init = synth.make(cfg, N=8192)
+    sh = _oracle_shifts(x, init, cfg.K, "bf16", 14)
+    i = next(j for j in range(1, len(sh)) if 0 < 2 * sh[j] <= min(sh[:j]))
+    tol = float(np.sqrt(sh[i] * min(sh[:i])))
+    o_n = i + 1
+    assert o_n == O.kmeans(x, cfg.K, 50, tol, init, "bf16")[2]
     xt, it = _T(x, "bf16"), _T(init, "bf16")
-    ids_a, c_a, n_a = batch_kmeans_Euclid(xt, cfg.K, max_iters=50, tol=1e-2, init_centroids=it)
-    assert 1 <= n_a < 50
+    ids_a, c_a, n_a = batch_kmeans_Euclid(xt, cfg.K, max_iters=50, tol=tol, init_centroids=it)
+    assert n_a == o_n, (n_a, o_n, tol, sh)
     ids_b, c_b, n_b = batch_kmeans_Euclid(xt, cfg.K, max_iters=n_a, tol=0.0, init_centroids=it)
     assert n_b == n_a
     assert torch.equal(ids_a, ids_b) and torch.equal(c_a, c_b)
     assert torch.equal(it, _T(init, "bf16")), "init_centroids was modified"
-    o_ids, o_c, o_n = O.kmeans(x, cfg.K, 50, 1e-2, init, "bf16")
-    assert abs(o_n - n_a) <= 1
+
+
+def test_loop_with_sort_recounts(monkeypatch):
+    """With a zero look-back spin budget every sort tile after the first
+    recounts its prefix from the pass's input; the Lloyd loop's result is
+    the same bits as with the normal look-back."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    cfg = synth.CONFIGS["c3"]
+    x, init = synth.make(cfg, N=65536)
+    xt, it = _T(x, "f16"), _T(init, "f16")
+    a = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
+    monkeypatch.setenv("FKC_SORT_SPIN", "0")
+    b = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
 def test_verbose_path_equals_fused_loop(capsys):

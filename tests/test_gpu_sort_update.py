@@ -40,7 +40,7 @@ SORT_CASES = [
 
 
 def _sort_ws(B, N, K):
-    """A label-sort workspace the test can inspect (health word = int32 0)."""
+    """A label-sort workspace the test can inspect (word 0 = recount count)."""
     from flash_kmeans_cuda import _lib
     n = _lib.lib.fkc_label_sort_workspace_bytes(B, N, K)
     ws = torch.full((n,), 0xA5, dtype=torch.uint8, device="cuda")  # stale bytes
@@ -238,3 +238,82 @@ def test_finalize_in_place():
     t = _t(old, "f16")
     _C.centroid_finalize(_t(sums, "f32"), _t(counts), t, out=t)
     assert np.array_equal(_np(t, "f16"), O.finalize(sums, counts, old, "f16"))
+
+
+@pytest.mark.parametrize("B,N,K,tile", [(1, 100000, 8192, 4096), (2, 70001, 70000, 1024),
+                                        (1, 524288, 8192, 4096), (3, 9000, 300, 256)])
+def test_label_sort_recount_path(monkeypatch, B, N, K, tile):
+    """With a zero look-back spin budget (FKC_SORT_SPIN=0) every tile after
+    the first stops waiting and recounts its prefix from the pass's input:
+    the output is still the stable sort, bit for bit, and the workspace's
+    first word counts the recounts (one per such tile and pass)."""
+    from flash_kmeans_cuda.ops import label_sort
+    monkeypatch.setenv("FKC_SORT_TILE", str(tile))
+    monkeypatch.setenv("FKC_SORT_SPIN", "0")
+    rng = np.random.default_rng(N + tile)
+    ids = rng.integers(-1, K + 1, (B, N)).astype(np.int32)
+    ws = _sort_ws(B, N, K)
+    s, p = label_sort(_t(ids), K, workspace=ws)
+    es, ep = O.label_sort(ids, K)
+    assert np.array_equal(_np(p), ep) and np.array_equal(_np(s), es)
+    ntiles = (N + tile - 1) // tile
+    bits = int(np.ceil(np.log2(K + 1)))
+    passes = (bits + 7) // 8
+    assert _health(ws) == B * passes * (ntiles - 1)
+    monkeypatch.delenv("FKC_SORT_SPIN")
+    s2, p2 = label_sort(_t(ids), K, workspace=ws)
+    assert torch.equal(s2, s) and torch.equal(p2, p) and _health(ws) == 0
+
+
+def _add_mode(x, perm, ids, K, dtype, indexed=True):
+    from flash_kmeans_cuda import _C
+    B, N, D = x.shape
+    sums = torch.zeros((B, K, D), device="cuda")
+    cnt = torch.zeros((B, K), device="cuda", dtype=torch.int32)
+    if indexed:
+        _C.centroid_update_sorted_indexed(_t(x, dtype), _t(perm), _t(ids), sums, cnt)
+    else:
+        rows = np.take_along_axis(x, perm.astype(np.int64)[..., None], 1)
+        _C.centroid_update_sorted(_t(rows, dtype), _t(ids), sums, cnt)
+    return _np(sums), _np(cnt)
+
+
+@pytest.mark.parametrize("indexed", [True, False])
+def test_update_invalid_labels_between_rows_of_one_label(indexed):
+    """Invalid labels between rows of one label, placed across 128-row unit
+    boundaries (..., 0, 0 | -1, 0, ...), split that label into several runs
+    in different waves; each run adds its share atomically, so counts are
+    exact and sums match the oracle (the reference's atomics accept any
+    order, update_sorted.cu:105,109)."""
+    B, N, K, D, dtype = 2, 40000, 40, 64, "f16"
+    rng = np.random.default_rng(17)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    ids = np.sort(rng.integers(0, K, (B, N)).astype(np.int32), axis=1)
+    for u in range(1, N // 128):
+        if u % 3 == 0:
+            ids[:, 128 * u] = -1
+        elif u % 3 == 1:
+            ids[:, 128 * u - 1] = K + 1
+    perm = np.stack([rng.permutation(N).astype(np.int32) for _ in range(B)])
+    es, ec = O.update_sorted_indexed(x, perm, ids, K, dtype)
+    s, c = _add_mode(x, perm, ids, K, dtype, indexed)
+    assert np.array_equal(c, ec)
+    tol = 1e-6 * np.maximum(ec[..., None], 1) * np.abs(O.to_f64(x, dtype)).max()
+    assert np.all(np.abs(s - es) <= tol + 1e-5)
+
+
+@pytest.mark.parametrize("K,D,dtype", [(37, 40, "bf16"), (3, 128, "f16"), (500, 7, "f32")])
+def test_update_unsorted_labels(K, D, dtype):
+    """Labels in no particular order: every run adds its share atomically,
+    so the totals are those of the same rows grouped by label."""
+    B, N = 1, 30000
+    rng = np.random.default_rng(K + D)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    ids = rng.integers(-1, K, (B, N)).astype(np.int32)
+    ids[:, 1000:9000] = K // 2          # one long run over many units
+    perm = np.stack([rng.permutation(N).astype(np.int32)])
+    es, ec = O.update_sorted_indexed(x, perm, ids, K, dtype)
+    s, c = _add_mode(x, perm, ids, K, dtype)
+    assert np.array_equal(c, ec)
+    tol = 1e-6 * np.maximum(ec[..., None], 1) * np.abs(O.to_f64(x, dtype)).max()
+    assert np.all(np.abs(s - es) <= tol + 1e-5)

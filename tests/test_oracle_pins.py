@@ -421,6 +421,133 @@ def test_loop_battery_rejects_planted_mistakes(mutant):
     assert _loop_battery(mutant) != []
 
 
+# ===================================================================== shift
+def _shift_battery(shift_fn):
+    """shift_fn(new, old, dtype) -> float, the convergence measure of
+    kmeans.py:104: max over every batch row and centroid of ||new - old||_2."""
+    fails = []
+    rng = _rng(21)
+    # 1. closed form.  Row deltas (3,4), (0,9) in row 0 and (6,8), (1,0) in
+    # row 1: the L2 norms are 5, 9, 10, 1, so the measure is 10 (row 1).  A
+    # squared norm gives 100, the mean 6.25, the L1 norm 14, the largest
+    # element 9, and a max over row 0 alone 9.
+    for dtype in ("f32", "f16", "bf16"):
+        old = np.array([[[1, 2], [4, -3]], [[-5, 0], [2, 2]]], np.float32)
+        delta = np.array([[[3, 4], [0, 9]], [[6, 8], [1, 0]]], np.float32)
+        new = O.from_f32(old + delta, dtype)
+        got = shift_fn(new, O.from_f32(old, dtype), dtype)
+        if got != 10.0:
+            fails.append(f"closed form {dtype}: {got!r}")
+    # no motion
+    c = O.from_f32(rng.standard_normal((2, 5, 8)).astype(np.float32), "f16")
+    if shift_fn(c, c.copy(), "f16") != 0.0:
+        fails.append("zero shift")
+    # 2. brute force on random rows (exact sums; float32 rounding only)
+    for dtype in ("f32", "f16", "bf16"):
+        old = O.from_f32(rng.standard_normal((3, 11, 7)).astype(np.float32), dtype)
+        new = O.from_f32(rng.standard_normal((3, 11, 7)).astype(np.float32), dtype)
+        of, nf = O.to_f32(old, dtype), O.to_f32(new, dtype)
+        want = max(brute.max_row_norm(_as_lists(nf[b]), _as_lists(of[b])) for b in range(3))
+        got = shift_fn(new, old, dtype)
+        if not np.isclose(got, want, rtol=2e-7, atol=0):
+            fails.append(f"brute {dtype}: {got!r} vs {want!r}")
+    return fails
+
+
+def _mut_shift_squared(new, old, dtype):
+    d = O.to_f64(new, dtype) - O.to_f64(old, dtype)
+    return float((d * d).sum(-1).max())
+
+
+def _mut_shift_mean(new, old, dtype):
+    d = O.to_f64(new, dtype) - O.to_f64(old, dtype)
+    return float(np.sqrt((d * d).sum(-1)).mean())
+
+
+def _mut_shift_l1(new, old, dtype):
+    d = O.to_f64(new, dtype) - O.to_f64(old, dtype)
+    return float(np.abs(d).sum(-1).max())
+
+
+def _mut_shift_linf(new, old, dtype):
+    d = O.to_f64(new, dtype) - O.to_f64(old, dtype)
+    return float(np.abs(d).max())
+
+
+def _mut_shift_first_row(new, old, dtype):
+    return O.shift(np.asarray(new)[:1], np.asarray(old)[:1], dtype)
+
+
+_SHIFT_MUTANTS = [_mut_shift_squared, _mut_shift_mean, _mut_shift_l1, _mut_shift_linf,
+                  _mut_shift_first_row]
+
+
+def test_shift_oracle_pinned():
+    assert _shift_battery(O.shift) == []
+
+
+@pytest.mark.parametrize("mutant", _SHIFT_MUTANTS)
+def test_shift_battery_rejects_planted_mistakes(mutant):
+    assert _shift_battery(mutant) != []
+
+
+def _kmeans_with_shift(shift_fn):
+    """O.kmeans with its convergence measure replaced (a planted mistake)."""
+    def run(x, K, iters, tol, init, dtype):
+        cur = np.array(init, copy=True)
+        ids, n = None, 0
+        for it in range(iters):
+            new, ids, _, _ = O.lloyd_step(x, cur, K, dtype)
+            n = it + 1
+            if tol > 0 and shift_fn(new, cur, dtype) < tol:
+                cur = new
+                break
+            cur = new
+        return ids, cur, n
+    return run
+
+
+def _stop_battery(kmeans_fn):
+    """The iteration the tol test stops at, where the answer depends on how
+    the shift is measured.  Two batch rows, the second moving more; the
+    shifts of every iteration are measured independently (brute-force norms
+    of the centroid trajectory), and tol is put between two consecutive
+    shifts below 1, so that a squared, mean, L1, largest-element or
+    first-row measure stops at another iteration."""
+    fails = []
+    rng = _rng(23)
+    B, N, K, D = 2, 300, 6, 3
+    x = rng.standard_normal((B, N, D))
+    x[1] *= 3.0
+    init = x[:, :K].copy()
+    traj = [init]
+    for it in range(1, 13):
+        traj.append(O.kmeans(x, K, it, 0.0, init, "f64")[1])
+    shifts = [max(brute.max_row_norm(_as_lists(traj[i][b]), _as_lists(traj[i - 1][b]))
+                  for b in range(B)) for i in range(1, len(traj))]
+    # first iteration i (1-based) whose shift is below 0.5 and still above the
+    # next one; tol halfway (geometric) between them
+    i = next(j for j in range(len(shifts) - 1)
+             if shifts[j] < 0.5 and shifts[j + 1] < shifts[j] and shifts[j + 1] > 0)
+    tol = float(np.sqrt(shifts[i] * shifts[i + 1]))
+    want_n = next(j + 1 for j, v in enumerate(shifts) if v < tol)
+    ids, cents, n = kmeans_fn(x, K, 50, tol, init, "f64")
+    if n != want_n:
+        fails.append(f"stopped after {n}, expected {want_n} (tol {tol:.3g})")
+    elif not np.allclose(cents, traj[want_n]):
+        fails.append("centroids at the stop differ from the trajectory")
+    return fails
+
+
+def test_tol_stop_iteration_pinned():
+    assert _stop_battery(O.kmeans) == []
+
+
+@pytest.mark.parametrize("mutant", _SHIFT_MUTANTS)
+def test_tol_stop_rejects_planted_shift_mistakes(mutant):
+    assert _stop_battery(_kmeans_with_shift(mutant)) != []
+
+
 # ==================================================================== quality
 def _quality_battery(inertia_fn, empty_fn):
     fails = []
@@ -438,10 +565,8 @@ def _quality_battery(inertia_fn, empty_fn):
                                           _as_lists(cf[b]), K)
             if not np.isclose(got[b], want, rtol=1e-13, atol=0):
                 fails.append(f"brute {dtype} b={b}: {got[b]!r} vs {want!r}")
-        e = empty_fn(ids, K)
-        for b in range(B):
-            if e[b] != brute.empty_clusters(list(map(int, ids[b])), K):
-                fails.append(f"empty {dtype} b={b}")
+        if empty_fn(ids, K) != brute.empty_clusters([list(map(int, r)) for r in ids], K):
+            fails.append(f"empty {dtype}")
     # 2. library: with labels from scipy's vq, inertia = sum of vq distances^2
     from scipy.cluster.vq import vq
     x = rng.standard_normal((1, 500, 16)).astype(np.float32)
@@ -460,8 +585,23 @@ def _quality_battery(inertia_fn, empty_fn):
     got = inertia_fn(x, np.array([[1, 0]], np.int32), c, "f32")
     if got[0] != 9.0:
         fails.append(f"known answer {got[0]}")
-    if empty_fn(np.array([[1, 0, 1]], np.int32), 3)[0] != 1:
+    if empty_fn(np.array([[1, 0, 1]], np.int32), 3) != 1:
         fails.append("known empty count")
+    # 4. the reference's own formula at B > 1 (quality_compare.py:86-88): one
+    # torch.bincount over the flattened labels; k is empty only when no row
+    # carries it (row 0 leaves 2 and 3 empty, row 1 fills 3)
+    import torch
+    ids = np.array([[0, 1, 1, 4], [3, 3, 0, 4]], np.int32)
+    want = int((torch.bincount(torch.from_numpy(ids).reshape(-1).long(), minlength=6) == 0)
+               .sum())
+    if want != 2 or empty_fn(ids, 6) != want:
+        fails.append("flattened bincount at B=2")
+    for trial in range(3):
+        ids = rng.integers(0, 40, (4, 25)).astype(np.int32)
+        want = int((torch.bincount(torch.from_numpy(ids).reshape(-1).long(), minlength=40)
+                    == 0).sum())
+        if empty_fn(ids, 40) != want:
+            fails.append(f"torch bincount trial {trial}")
     return fails
 
 
@@ -488,7 +628,12 @@ def _mut_norm_not_squared(x, ids, c, dtype):
 
 
 def _mut_empty_off_by_one(ids, K):
-    return O.empty_clusters(ids, K) - (ids == K - 1).any(axis=1)
+    return O.empty_clusters(ids, K) - int((np.asarray(ids) == K - 1).any())
+
+
+def _mut_empty_per_row(ids, K):
+    # empty (b, k) pairs summed over rows, instead of one flattened histogram
+    return sum(O.empty_clusters(np.asarray(ids)[b:b + 1], K) for b in range(len(ids)))
 
 
 def test_quality_oracle_pinned():
@@ -500,5 +645,79 @@ def test_quality_battery_rejects_planted_inertia_mistakes(mutant):
     assert _quality_battery(mutant, O.empty_clusters) != []
 
 
-def test_quality_battery_rejects_planted_empty_count_mistake():
-    assert _quality_battery(O.assigned_inertia, _mut_empty_off_by_one) != []
+@pytest.mark.parametrize("mutant", [_mut_empty_off_by_one, _mut_empty_per_row])
+def test_quality_battery_rejects_planted_empty_count_mistakes(mutant):
+    assert _quality_battery(O.assigned_inertia, mutant) != []
+
+
+# ============================================================ sampled inertia
+def _sample_battery(fn):
+    """fn(x, c, sample_idx, dtype) -> float (quality_compare.py:91-116)."""
+    fails = []
+    rng = _rng(13)
+    # 1. brute force: exact nearest squared distance of every sampled point,
+    # summed over batch rows (the GEMM-form float32 distance differs from it
+    # by float32 rounding only)
+    for dtype in ("f32", "f16", "bf16"):
+        B, N, K, D = 2, 50, 7, 6
+        x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32) * 2, dtype)
+        c = O.from_f32(rng.standard_normal((B, K, D)).astype(np.float32) * 2, dtype)
+        idx = rng.permutation(N)[:17]
+        xf, cf = O.to_f32(x, dtype), O.to_f32(c, dtype)
+        want = sum(brute.nearest_sqdist(list(map(float, xf[b, n])), _as_lists(cf[b]))
+                   for b in range(B) for n in idx)
+        got = fn(x, c, idx, dtype)
+        if not np.isclose(got, want, rtol=1e-5, atol=1e-4):
+            fails.append(f"brute {dtype}: {got!r} vs {want!r}")
+    # 2. library: scipy's vq distances of the sample
+    from scipy.cluster.vq import vq
+    x = rng.standard_normal((1, 400, 12)).astype(np.float32)
+    c = rng.standard_normal((1, 30, 12)).astype(np.float32)
+    idx = rng.permutation(400)[:64]
+    _, dist = vq(x[0, idx].astype(np.float64), c[0].astype(np.float64))
+    if not np.isclose(fn(x, c, idx, "f32"), (dist ** 2).sum(), rtol=1e-5):
+        fails.append("scipy vq")
+    # 3. known answers: sampled points that are centroids give 0 (clamped);
+    # a point at distance 3 from the nearest of two centroids gives 9
+    c = np.array([[[0.0, 0.0], [10.0, 0.0]]], np.float32)
+    x = np.array([[[10.0, 0.0], [0.0, 3.0], [0.0, 0.0], [7.0, 0.0]]], np.float32)
+    if fn(x, c, np.array([0, 2]), "f32") != 0.0:
+        fails.append("centroids as samples")
+    if fn(x, c, np.array([1, 3]), "f32") != 18.0:
+        fails.append("known distances 3 and 3")
+    if fn(x, c, np.array([1]), "f32") != 9.0:
+        fails.append("only the sampled points count")
+    return fails
+
+
+def _mut_sample_max_centroid(x, c, idx, dtype):
+    xs, cf = O.to_f64(np.asarray(x)[:, idx], dtype), O.to_f64(c, dtype)
+    return float(sum(((xs[b][:, None] - cf[b][None]) ** 2).sum(-1).max(-1).sum()
+                     for b in range(xs.shape[0])))
+
+
+def _mut_sample_first_row_only(x, c, idx, dtype):
+    return O.sample_exact_inertia(np.asarray(x)[:1], np.asarray(c)[:1], idx, dtype)
+
+
+def _mut_sample_no_csq(x, c, idx, dtype):
+    xs, cf = O.to_f64(np.asarray(x)[:, idx], dtype), O.to_f64(c, dtype)
+    tot = 0.0
+    for b in range(xs.shape[0]):
+        d = (xs[b] ** 2).sum(-1)[:, None] - 2.0 * xs[b] @ cf[b].T
+        tot += float(np.maximum(d.min(-1), 0).sum())
+    return tot
+
+
+def _mut_sample_all_points(x, c, idx, dtype):
+    return O.sample_exact_inertia(x, c, np.arange(np.asarray(x).shape[1]), dtype)
+
+
+def test_sample_exact_inertia_oracle_pinned():
+    assert _sample_battery(O.sample_exact_inertia) == []
+
+
+@pytest.mark.parametrize("mutant", [_mut_sample_max_centroid, _mut_sample_first_row_only,
+                                    _mut_sample_no_csq, _mut_sample_all_points])
+def test_sample_battery_rejects_planted_mistakes(mutant):
+    assert _sample_battery(mutant) != []
