@@ -253,8 +253,10 @@ def _report(configs) -> int:
     """Per-configuration measurements (one JSON line each, then a markdown
     table): assign alone (median of 7 x 10 launches, HIP events), the Lloyd
     loop's steady state (cfg.iters iterations, tol = 0, per iteration), the
-    reference's methodology (one whole call with max_iters=1, best of 5), and
-    the roofline fraction ideal / measured per iteration."""
+    reference's methodology (one whole call with max_iters=1, best of 5), the
+    roofline fraction ideal / measured per iteration, and the CPU oracle's
+    ms/iter on the same inputs (2 iterations on every point, BLAS threads
+    stated)."""
     import statistics
     import torch
     from flash_kmeans_cuda import _C, batch_kmeans_Euclid, synth
@@ -297,6 +299,9 @@ def _report(configs) -> int:
             torch.cuda.synchronize()
             one.append((time.perf_counter() - t0) * 1e3)
         flops, byts, ideal = _ideal_ms(cfg)
+        # The CPU oracle on the same inputs: 2 iterations on every point
+        # (the loop's fp32 BLAS form), a few seconds per config at most.
+        cpu = _cpu_baseline(cfg, x_np, init_np, 0, 2)
         row = {
             "config": name, "B": cfg.B, "N": cfg.N, "K": cfg.K, "D": cfg.D,
             "dtype": cfg.dtype, "assign_ms": round(assign_ms, 5),
@@ -307,17 +312,21 @@ def _report(configs) -> int:
             "roofline_frac": round(ideal / steady, 4),
             "ref_ms_per_iter": REF_MS_PER_ITER.get(name),
             "ref_assign_tflops": REF_ASSIGN_TFLOPS.get(name),
+            "cpu_ms_per_iter": round(cpu["value"], 3),
+            "cpu_cores": cpu["cores"],
         }
         rows.append(row)
         print(json.dumps(row), flush=True)
     print("| config | (B, N, K, D) dtype | assign ms | assign TFLOP/s | ms/iter steady | "
-          "ms/iter one call | ideal ms/iter | ideal/measured | reference ms/iter (RTX 4090) |")
-    print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
+          "ms/iter one call | ideal ms/iter | ideal/measured | reference ms/iter (RTX 4090) | "
+          "CPU oracle ms/iter (threads) |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|")
     for r in rows:
         print(f"| {r['config']} | ({r['B']}, {r['N']}, {r['K']}, {r['D']}) {r['dtype']} | "
               f"{r['assign_ms']:.4f} | {r['assign_tflops']:.1f} | {r['ms_per_iter_steady']:.4f} | "
               f"{r['ms_per_iter_ref_method']:.4f} | {r['ideal_ms_per_iter']:.4f} | "
-              f"{r['roofline_frac']:.3f} | {r['ref_ms_per_iter'] or '—'} |", flush=True)
+              f"{r['roofline_frac']:.3f} | {r['ref_ms_per_iter'] or '—'} | "
+              f"{r['cpu_ms_per_iter']:.1f} ({r['cpu_cores']}) |", flush=True)
     return 0
 
 

@@ -91,6 +91,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #ifndef FKC_KC_DMA8
 #define FKC_KC_DMA8 128
 #endif
+#ifndef FKC_KC_DMA_SAVE
+#define FKC_KC_DMA_SAVE 128
+#endif
 #ifndef FKC_SLICE_MIN_ROWS
 #define FKC_SLICE_MIN_ROWS 2048
 #endif
@@ -151,12 +154,30 @@ __device__ inline void fold_exact(const f32x4& acc, float& best, int& bidx,
   best = nb;
 }
 
+// Block fold that also keeps the lane's four scores of the block where its
+// running maximum was first reached, so the winning row is known at the end
+// without re-scoring: the first of the four saved scores equal to the best.
+// Four register selects per four scores more than fold_block; used where
+// the grid leaves registers spare (two waves per SIMD).
+__device__ inline void fold_saved(const f32x4& acc, float& best, int& bblk,
+                                  f32x4& saved, int blk) {
+  const float nb = fmaxf(fmaxf(fmaxf(fmaxf(best, acc[0]), acc[1]), acc[2]),
+                         acc[3]);
+  const bool up = nb > best;  // strict: equal later scores keep the first
+  bblk = up ? blk : bblk;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) saved[j] = up ? acc[j] : saved[j];
+  best = nb;
+}
+
 // DS2: 32-feature steps (padded width DP = 32*DS2 >= D); PT: 16-point tiles
 // per wave; PAD: D < DP, so segments past D read as zeros (a compile-time
 // flag: the unpadded variants carry no per-load condition); EXACT: track
-// the exact index in the loop instead of re-scoring at the end.  D % 8 == 0
-// so every 8-feature segment is a 16-byte load.
-template <int DT, int DS2, int PT, bool PAD, bool EXACT>
+// the exact index in the loop instead of re-scoring at the end; SAVE: keep
+// the best block's scores (fold_saved) instead of re-scoring at the end
+// (two waves per SIMD, 128-row stages).  D % 8 == 0 so every 8-feature
+// segment is a 16-byte load.
+template <int DT, int DS2, int PT, bool PAD, bool EXACT, bool SAVE>
 __global__ void __launch_bounds__(THREADS,
                                   PT == 8 ? 2
                                   : (DS2 == 2 && PT <= 4) ? 4
@@ -219,10 +240,12 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
 
   float best[PT];
   int bblk[PT];
+  f32x4 sv[SAVE ? PT : 1];  // SAVE: the lane's scores of its best block
 #pragma unroll
   for (int p = 0; p < PT; ++p) {
     best[p] = -INFINITY;
     bblk[p] = 0;
+    if constexpr (SAVE) sv[p] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   }
 
   // Fold one 16-centroid block's accumulators into the running maxima.
@@ -231,6 +254,8 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     for (int p = 0; p < PT; ++p) {
       if constexpr (EXACT)
         fold_exact(acc[p], best[p], bblk[p], blk + 4 * g);
+      else if constexpr (SAVE)
+        fold_saved(acc[p], best[p], bblk[p], sv[SAVE ? p : 0], blk);
       else
         fold_block(acc[p], best[p], bblk[p], blk);
     }
@@ -261,6 +286,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // 0.021 ms at (2, 30000, 2000, 32); D = 64: 128 rows, ~1%), so a stage
     // still spans enough matrix work to hide its barrier.
     constexpr int KCD0 = PT == 8    ? FKC_KC_DMA8
+                         : SAVE     ? FKC_KC_DMA_SAVE
                          : DS2 == 1 ? 4 * FKC_KC_DMA
                          : DS2 == 2 ? 2 * FKC_KC_DMA
                          : DS2 <= 4 ? FKC_KC_DMA
@@ -431,7 +457,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
 #pragma unroll
             for (int i = 0; i < DS2 * PT; ++i) {
               __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-              __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+              __builtin_amdgcn_sched_group_barrier(0x002, SAVE ? 2 : 1, 0);  // VALU
             }
           }
 #pragma unroll
@@ -575,6 +601,40 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     }
     return;
   }
+  if constexpr (SAVE) {
+    // The winning row of each lane is the first of its saved scores equal
+    // to its best; the four lanes of a point then keep the higher score,
+    // ties to the lower row (lane rows do not interleave within a block, and
+    // an earlier block has lower rows).  min() only guards degenerate input
+    // (every score -inf or NaN): the label stays a valid row.
+#pragma unroll
+    for (int p = 0; p < PT; ++p) {
+      float bv = best[p];
+      const f32x4 v = sv[SAVE ? p : 0];
+      const int j = v[0] == bv ? 0 : (v[1] == bv ? 1 : (v[2] == bv ? 2 : 3));
+      int bi = min(bblk[p] + 4 * g + j, K - 1);
+#pragma unroll
+      for (int off = 16; off <= 32; off <<= 1) {
+        const float ob = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ob > bv || (ob == bv && oi < bi)) {
+          bv = ob;
+          bi = oi;
+        }
+      }
+      const int n = n0 + 16 * p + col;
+      if (g == 0 && n < N) {
+        if (psc != nullptr) {
+          const size_t o = ((size_t)b * gridDim.z + blockIdx.z) * N + n;
+          psc[o] = bv;
+          pidx[o] = k0 + bi;
+        } else {
+          ids[(size_t)b * N + n] = bi;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int p = 0; p < PT; ++p) {
     float bv = best[p];
@@ -588,7 +648,28 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
         base = obase;
       }
     }
-    // Accumulator rows 4g+j of this lane belong to point 4g+j of the tile.
+    // Every load of the re-score is issued before any of them is used:
+    // unconditional, from rows clamped to K - 1 (a clamped row only stands
+    // for a candidate past K, whose seed is -inf below), so the tile costs
+    // one memory round trip rather than one per load.  Each lane loads its
+    // own point's four candidate rows (its segments of them) and their c_sq.
+    float cq[4];
+    u32x4 ar[4][DS2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kr = min(base + r, K - 1);
+      cq[r] = qb[kr];
+      const u32x4* crow = reinterpret_cast<const u32x4*>(cb + (size_t)kr * D);
+#pragma unroll
+      for (int s = 0; s < DS2; ++s) {
+        const int seg = 4 * s + g;
+        // Padded widths load an in-bounds segment and zero it past D.
+        const u32x4 v = crow[padded ? min(seg, dsegs - 1) : seg];
+        ar[r][s] = (!padded || seg < dsegs) ? v : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    // Accumulator rows 4g+j of this lane belong to point 4g+j of the tile;
+    // lane 4g+j (g = 0 there) holds that point's base and candidate c_sq.
     int rbase[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) rbase[j] = __shfl(base, 4 * g + j, 64);
@@ -599,18 +680,11 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       f32x4 acc;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int k = rbase[j] + r;
-        acc[j] = k < K ? -0.5f * qb[k] : -INFINITY;
+        const float q = __shfl(cq[r], 4 * g + j, 64);
+        acc[j] = rbase[j] + r < K ? -0.5f * q : -INFINITY;
       }
-      const int kr = min(base + r, K - 1);
-      const u32x4* crow = reinterpret_cast<const u32x4*>(cb + (size_t)kr * D);
 #pragma unroll
-      for (int s = 0; s < DS2; ++s) {
-        const int seg = 4 * s + g;
-        const u32x4 a =
-            (!padded || seg < dsegs) ? crow[seg] : u32x4{0u, 0u, 0u, 0u};
-        acc = mfma16<DT>(a, xr[p][s], acc);
-      }
+      for (int s = 0; s < DS2; ++s) acc = mfma16<DT>(ar[r][s], xr[p][s], acc);
       float d = acc[0];
       d = e == 1 ? acc[1] : d;
       d = e == 2 ? acc[2] : d;
@@ -675,7 +749,7 @@ struct Slices {
 // ev0 / ev1 (both null or both set): events that the dispatch packets
 // themselves stamp, ev0 at the start of the scoring kernel and ev1 at the
 // end of the last kernel (no marker packets in the stream).
-template <int DT, int DS2, int PT, bool PAD, bool EXACT>
+template <int DT, int DS2, int PT, bool PAD, bool EXACT, bool SAVE>
 int launch_mfma_t(const void* x, const void* c, const float* c_sq,
                   int32_t* ids, int64_t B, int64_t N, int64_t K, int64_t D,
                   const int32_t* ctrl, const Slices& sl, hipStream_t s,
@@ -686,13 +760,13 @@ int launch_mfma_t(const void* x, const void* c, const float* c_sq,
             (unsigned)sl.S);
   const int kspan = merge ? sl.kspan : (int)K;
   if (ev0 != nullptr)
-    hipExtLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
+    hipExtLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT, SAVE>), grid,
                           dim3(THREADS), 0, s, ev0, merge ? nullptr : ev1, 0,
                           static_cast<const uint16_t*>(x),
                           static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
                           (int)K, (int)D, ctrl, kspan, sl.psc, sl.pidx);
   else
-    hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT>), grid,
+    hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT, SAVE>), grid,
                        dim3(THREADS), 0, s, static_cast<const uint16_t*>(x),
                        static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
                        (int)K, (int)D, ctrl, kspan, sl.psc, sl.pidx);
@@ -714,19 +788,27 @@ using MfmaLauncher = int (*)(const void*, const void*, const float*, int32_t*,
                              hipEvent_t, hipEvent_t);
 
 template <int DT, int DS2, int PT>
-constexpr MfmaLauncher entry(bool pad, bool exact) {
+constexpr MfmaLauncher entry(bool pad, bool exact, bool save) {
   if constexpr (PT == 8) {
     // Direct stages and the re-score epilogue only (DS2 = 4, unpadded).
     if constexpr (DS2 == 4) {
-      if (!pad && !exact) return &launch_mfma_t<DT, DS2, PT, false, false>;
+      if (!pad && !exact && !save)
+        return &launch_mfma_t<DT, DS2, PT, false, false, false>;
     }
     return nullptr;
   } else if constexpr (PT * DS2 * 4 <= 64) {
+    if (save) {
+      // Saved-score fold: four tiles at D = 97..128, unpadded only.
+      if constexpr (PT == 4 && DS2 == 4) {
+        if (!pad && !exact) return &launch_mfma_t<DT, DS2, PT, false, false, true>;
+      }
+      return nullptr;
+    }
     if (exact)
-      return pad ? &launch_mfma_t<DT, DS2, PT, true, true>
-                 : &launch_mfma_t<DT, DS2, PT, false, true>;
-    return pad ? &launch_mfma_t<DT, DS2, PT, true, false>
-               : &launch_mfma_t<DT, DS2, PT, false, false>;
+      return pad ? &launch_mfma_t<DT, DS2, PT, true, true, false>
+                 : &launch_mfma_t<DT, DS2, PT, false, true, false>;
+    return pad ? &launch_mfma_t<DT, DS2, PT, true, false, false>
+               : &launch_mfma_t<DT, DS2, PT, false, false, false>;
   } else {
     return nullptr;
   }
@@ -736,35 +818,35 @@ constexpr MfmaLauncher entry(bool pad, bool exact) {
 // re-score epilogue).  The 1/2/4 variants keep the point registers
 // (PT * DS2 * 4 VGPRs) at <= 64; the eight-tile one holds 128.
 template <int DT, int DS2>
-MfmaLauncher by_pt(int pt, bool pad, bool exact) {
+MfmaLauncher by_pt(int pt, bool pad, bool exact, bool save) {
   switch (pt) {
-    case 1: return entry<DT, DS2, 1>(pad, exact);
-    case 2: return entry<DT, DS2, 2>(pad, exact);
-    case 4: return entry<DT, DS2, 4>(pad, exact);
-    case 8: return entry<DT, DS2, 8>(pad, exact);
+    case 1: return entry<DT, DS2, 1>(pad, exact, save);
+    case 2: return entry<DT, DS2, 2>(pad, exact, save);
+    case 4: return entry<DT, DS2, 4>(pad, exact, save);
+    case 8: return entry<DT, DS2, 8>(pad, exact, save);
     default: return nullptr;
   }
 }
 
 template <int DT>
-MfmaLauncher mfma_launcher(int ds2, int pt, bool pad, bool exact) {
+MfmaLauncher mfma_launcher(int ds2, int pt, bool pad, bool exact, bool save) {
   switch (ds2) {
-    case 1: return by_pt<DT, 1>(pt, pad, exact);
-    case 2: return by_pt<DT, 2>(pt, pad, exact);
-    case 3: return by_pt<DT, 3>(pt, pad, exact);
-    case 4: return by_pt<DT, 4>(pt, pad, exact);
-    case 5: return by_pt<DT, 5>(pt, pad, exact);
-    case 6: return by_pt<DT, 6>(pt, pad, exact);
-    case 7: return by_pt<DT, 7>(pt, pad, exact);
-    case 8: return by_pt<DT, 8>(pt, pad, exact);
-    case 9: return by_pt<DT, 9>(pt, pad, exact);
-    case 10: return by_pt<DT, 10>(pt, pad, exact);
-    case 11: return by_pt<DT, 11>(pt, pad, exact);
-    case 12: return by_pt<DT, 12>(pt, pad, exact);
-    case 13: return by_pt<DT, 13>(pt, pad, exact);
-    case 14: return by_pt<DT, 14>(pt, pad, exact);
-    case 15: return by_pt<DT, 15>(pt, pad, exact);
-    case 16: return by_pt<DT, 16>(pt, pad, exact);
+    case 1: return by_pt<DT, 1>(pt, pad, exact, save);
+    case 2: return by_pt<DT, 2>(pt, pad, exact, save);
+    case 3: return by_pt<DT, 3>(pt, pad, exact, save);
+    case 4: return by_pt<DT, 4>(pt, pad, exact, save);
+    case 5: return by_pt<DT, 5>(pt, pad, exact, save);
+    case 6: return by_pt<DT, 6>(pt, pad, exact, save);
+    case 7: return by_pt<DT, 7>(pt, pad, exact, save);
+    case 8: return by_pt<DT, 8>(pt, pad, exact, save);
+    case 9: return by_pt<DT, 9>(pt, pad, exact, save);
+    case 10: return by_pt<DT, 10>(pt, pad, exact, save);
+    case 11: return by_pt<DT, 11>(pt, pad, exact, save);
+    case 12: return by_pt<DT, 12>(pt, pad, exact, save);
+    case 13: return by_pt<DT, 13>(pt, pad, exact, save);
+    case 14: return by_pt<DT, 14>(pt, pad, exact, save);
+    case 15: return by_pt<DT, 15>(pt, pad, exact, save);
+    case 16: return by_pt<DT, 16>(pt, pad, exact, save);
     default: return nullptr;
   }
 }
@@ -813,8 +895,19 @@ static int choose_pt(int ds2, bool pad, bool exact, int64_t B, int64_t N) {
 
 struct Plan {
   int ds2, pt, S, kspan;
-  bool pad, exact;
+  bool pad, exact, save;
 };
+
+// The saved-score fold (four tiles at D = 97..128, unpadded) runs at two
+// waves per SIMD; it is taken where the launch has at most two workgroups
+// per CU anyway (grids of <= 512 workgroups), so the spare registers cost
+// no occupancy.  FKC_SAVE=0/1 forces it off / on where it exists.
+static bool use_save(const Plan& p, int64_t wgs) {
+  if (p.pt != 4 || p.ds2 != 4 || p.pad || p.exact) return false;
+  const int o = save_override();
+  if (o >= 0) return o == 1;
+  return wgs <= 512;
+}
 
 // Launch plan.  K is sliced only when no unsliced grid fills the chip (few
 // points, many centroids): the most tiles the point budget allows (four up
@@ -842,6 +935,7 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   p.pt = choose_pt(p.ds2, p.pad, p.exact, B, N);
   p.S = 1;
   p.kspan = (int)K;
+  p.save = use_save(p, grid_wgs(p.pt, B, N));
   if (!can_slice || p.exact) return p;
   // Four tiles, not eight: on sliced-size grids four tiles on ~256
   // workgroups beat eight on 512 (N = 8192, K = 65536: 0.150 vs 0.166 ms;
@@ -875,6 +969,7 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   p.pt = pt;
   p.S = (int)S;
   p.kspan = (int)span;
+  p.save = use_save(p, tiles * S);
   return p;
 }
 
@@ -911,8 +1006,9 @@ int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
     return fail(FKC_ERR_WORKSPACE, "assign: workspace %zu < %zu bytes",
                 ws_bytes, need);
   MfmaLauncher fn =
-      dtype == FKC_F16 ? mfma_launcher<FKC_F16>(p.ds2, p.pt, p.pad, p.exact)
-                       : mfma_launcher<FKC_BF16>(p.ds2, p.pt, p.pad, p.exact);
+      dtype == FKC_F16
+          ? mfma_launcher<FKC_F16>(p.ds2, p.pt, p.pad, p.exact, p.save)
+          : mfma_launcher<FKC_BF16>(p.ds2, p.pt, p.pad, p.exact, p.save);
   if (!fn)
     return fail(FKC_ERR_UNSUPPORTED, "assign: no MFMA variant for D=%lld",
                 (long long)D);

@@ -65,6 +65,12 @@ int sort_tile_override() {
   return (v == 256 || v == 512 || v == 1024 || v == 2048 || v == 4096) ? v : 0;
 }
 
+int save_override() {
+  const char* s = std::getenv("FKC_SAVE");
+  if (!s || !*s) return -1;
+  return std::strcmp(s, "1") == 0 ? 1 : (std::strcmp(s, "0") == 0 ? 0 : -1);
+}
+
 int sort_spin_override(int dflt) {
   const char* s = std::getenv("FKC_SORT_SPIN");
   if (!s || !*s) return dflt;

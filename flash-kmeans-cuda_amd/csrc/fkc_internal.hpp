@@ -166,5 +166,8 @@ int launch_sampled_inertia(const void* x, const void* c, const int32_t* idx,
 int ntiles_override();
 // FKC_KSPLIT=1..64: centroid slices of a sliced MFMA assign; 0 = auto.
 int ksplit_override();
+// FKC_SAVE=0|1: saved-score fold of the four-tile D = 97..128 assign off /
+// on where it exists; -1 = auto.
+int save_override();
 
 }  // namespace fkc

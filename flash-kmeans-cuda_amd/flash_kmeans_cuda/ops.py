@@ -1,10 +1,16 @@
-"""Thin Python wrappers around the gfx950 kernels (mirror of the reference's
-flash_kmeans_cuda/ops.py:30-130, same names, arguments and errors).
+"""Per-operation entry points of the K-Means hot path.
 
-Differences, all internal: the labels are sorted by this library's stable
-radix sort instead of torch.sort (ops.py:89), the centroid update always
-reads x through the sorted permutation (no gathered copy of x), and c_sq is
-computed by a HIP kernel.
+These keep the reference's public names, argument meaning, return values and
+error classes (flash_kmeans_cuda/ops.py:30-130): `euclid_assign`,
+`centroid_update_sorted` and `centroid_finalize`, plus `label_sort` and
+`row_sqnorm`, which expose two steps the reference does with torch ops.
+Host tensors raise ValueError; everything else is checked by the `_C` layer
+and by the C ABI underneath (RuntimeError).
+
+Internally the labels are ordered by this library's stable radix sort (the
+reference calls torch.sort, ops.py:89), the update always reads x through the
+sorted permutation (no gathered copy of x is made), and c_sq comes from a HIP
+kernel rather than a torch expression.
 """
 
 from __future__ import annotations
@@ -16,23 +22,27 @@ import torch
 from . import _C, _lib
 
 
-def _ensure_contig(t: torch.Tensor, name: str) -> torch.Tensor:
-    if not t.is_cuda:
-        raise ValueError(f"{name} must be a CUDA tensor (got {t.device})")
-    if not t.is_contiguous():
-        return t.contiguous()
-    return t
+def _gpu_dense(name: str, t: torch.Tensor) -> torch.Tensor:
+    """`t` itself when it is a dense GPU tensor, a dense copy when it is a
+    strided view; host tensors are refused with ValueError (as the reference
+    refuses them, ops.py:23-24)."""
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: expected a tensor on a GPU device, found one on {t.device}")
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _as_i32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.int32 else t.to(torch.int32)
 
 
 def row_sqnorm(t: torch.Tensor) -> torch.Tensor:
-    """(..., D) -> (...) fp32 sum of squares of the stored values."""
-    t = _ensure_contig(t, "t")
-    D = t.shape[-1]
+    """Squared Euclidean norm of every row of a (..., D) tensor, summed in
+    fp32 over the stored element values; shape (...)."""
+    t = _gpu_dense("t", t)
     out = torch.empty(t.shape[:-1], dtype=torch.float32, device=t.device)
-    rows = out.numel()
-    _lib.check(_lib.lib.fkc_row_sqnorm(t.data_ptr(), out.data_ptr(), rows, D,
-                                       _lib.dtype_code(t.dtype), _lib.stream_of(t)),
-               "row_sqnorm")
+    _lib.check(_lib.lib.fkc_row_sqnorm(t.data_ptr(), out.data_ptr(), out.numel(),
+                                       t.shape[-1], _lib.dtype_code(t.dtype),
+                                       _lib.stream_of(t)), "row_sqnorm")
     return out
 
 
@@ -43,24 +53,19 @@ def euclid_assign(
     c_sq: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Assign each point to its nearest centroid (Euclidean).
+    """Label of the closest centroid for every point.
 
-    Args:
-        x: (B, N, D) fp16/bf16/fp32, CUDA.
-        centroids: (B, K, D) same dtype as x.
-        x_sq: (B, N) fp32 ||x||^2 per point (read only by the fp32 route).
-        c_sq: (B, K) fp32 ||c||^2 per centroid; computed if None.
-        out: optional (B, N) int32 buffer to write into.
-
-    Returns:
-        cluster_ids: (B, N) int32.
+    x (B, N, D) and centroids (B, K, D) share one dtype: fp16, bf16 or fp32.
+    x_sq (B, N) and c_sq (B, K) hold the fp32 squared row norms; x_sq only
+    matters on the fp32 route (the matrix-core route ranks by
+    c_sq - 2<x, c>), and c_sq is computed here when omitted.  The labels,
+    int32 (B, N), are written to `out` when given; equal distances go to the
+    lower centroid index.
     """
-    x = _ensure_contig(x, "x")
-    centroids = _ensure_contig(centroids, "centroids")
-    x_sq = _ensure_contig(x_sq, "x_sq").to(torch.float32)
-    if c_sq is None:
-        c_sq = row_sqnorm(centroids)
-    c_sq = _ensure_contig(c_sq, "c_sq").to(torch.float32)
+    x = _gpu_dense("x", x)
+    centroids = _gpu_dense("centroids", centroids)
+    x_sq = _gpu_dense("x_sq", x_sq).float()
+    c_sq = row_sqnorm(centroids) if c_sq is None else _gpu_dense("c_sq", c_sq).float()
     return _C.euclid_assign(x, centroids, x_sq, c_sq, out)
 
 
@@ -75,9 +80,7 @@ def label_sort(cluster_ids: torch.Tensor, K: int, *,
     out and that recounted their prefix instead (a diagnostic: the output is
     valid either way).
     """
-    cluster_ids = _ensure_contig(cluster_ids, "cluster_ids")
-    if cluster_ids.dtype != torch.int32:
-        cluster_ids = cluster_ids.to(torch.int32)
+    cluster_ids = _as_i32(_gpu_dense("cluster_ids", cluster_ids))
     B, N = cluster_ids.shape
     sorted_ids = torch.empty_like(cluster_ids)
     perm = torch.empty_like(cluster_ids)
@@ -104,34 +107,23 @@ def centroid_update_sorted(
     sums_out: Optional[torch.Tensor] = None,
     counts_out: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Sort cluster_ids along N, then accumulate per-cluster sums/counts.
+    """Per-cluster fp32 row sums (B, K, D) and int32 counts (B, K) of x under
+    labels given in any order.
 
-    Args:
-        x: (B, N, D) compute dtype.
-        cluster_ids: (B, N) int32 (any order).
-        K: number of clusters.
-        sums_out: optional (B, K, D) fp32 (zeroed here).
-        counts_out: optional (B, K) int32 (zeroed here).
-
-    Returns:
-        (centroid_sums, centroid_counts).
+    The labels are sorted first; the sums are taken over each label's rows
+    in that order.  Buffers passed as sums_out / counts_out are cleared and
+    filled; otherwise new ones are returned.
     """
-    x = _ensure_contig(x, "x")
-    cluster_ids = _ensure_contig(cluster_ids, "cluster_ids")
-    if cluster_ids.dtype != torch.int32:
-        cluster_ids = cluster_ids.to(torch.int32)
+    x = _gpu_dense("x", x)
+    cluster_ids = _as_i32(_gpu_dense("cluster_ids", cluster_ids))
     B, N, D = x.shape
     sorted_ids, perm = label_sort(cluster_ids, K)
-    if sums_out is None:
-        sums_out = torch.zeros((B, K, D), device=x.device, dtype=torch.float32)
-    else:
-        sums_out.zero_()
-    if counts_out is None:
-        counts_out = torch.zeros((B, K), device=x.device, dtype=torch.int32)
-    else:
-        counts_out.zero_()
-    _C.centroid_update_sorted_indexed(x, perm, sorted_ids, sums_out, counts_out)
-    return sums_out, counts_out
+    sums = (torch.zeros((B, K, D), device=x.device, dtype=torch.float32)
+            if sums_out is None else sums_out.zero_())
+    counts = (torch.zeros((B, K), device=x.device, dtype=torch.int32)
+              if counts_out is None else counts_out.zero_())
+    _C.centroid_update_sorted_indexed(x, perm, sorted_ids, sums, counts)
+    return sums, counts
 
 
 def centroid_finalize(
@@ -140,13 +132,9 @@ def centroid_finalize(
     old_centroids: torch.Tensor,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """new[b,k] = sums[b,k] / counts[b,k] if counts > 0 else old_centroids[b,k].
-
-    Casts back to old_centroids.dtype.
-    """
-    return _C.centroid_finalize(
-        centroid_sums.contiguous(),
-        centroid_counts.contiguous(),
-        old_centroids.contiguous(),
-        out,
-    )
+    """New centroids in old_centroids' dtype: the mean sums / counts for
+    clusters with points, the old centroid for empty ones (the mean is an
+    IEEE fp32 division rounded to nearest)."""
+    dense = [t if t.is_contiguous() else t.contiguous()
+             for t in (centroid_sums, centroid_counts, old_centroids)]
+    return _C.centroid_finalize(*dense, out)

@@ -29,12 +29,12 @@ from typing import Dict
 import torch
 
 from . import _lib
-from .ops import _ensure_contig, euclid_assign, row_sqnorm
+from .ops import _gpu_dense, euclid_assign, row_sqnorm
 
 
 def _check_pair(x: torch.Tensor, cents: torch.Tensor, what: str):
-    x = _ensure_contig(x, "x")
-    cents = _ensure_contig(cents, "centroids")
+    x = _gpu_dense("x", x)
+    cents = _gpu_dense("centroids", cents)
     if x.dim() != 3 or cents.dim() != 3 or cents.shape[0] != x.shape[0] or \
             cents.shape[2] != x.shape[2]:
         raise RuntimeError(f"{what}: shapes must be x (B,N,D), centroids (B,K,D)")
@@ -44,7 +44,7 @@ def _check_pair(x: torch.Tensor, cents: torch.Tensor, what: str):
 
 
 def _run(x, ids: torch.Tensor, cents, K: int, want_inertia: bool):
-    ids = _ensure_contig(ids, "ids")
+    ids = _gpu_dense("ids", ids)
     if ids.dtype != torch.int32:
         ids = ids.to(torch.int32)
     B, N = ids.shape
@@ -106,7 +106,7 @@ def sampled_inertia(x: torch.Tensor, cents: torch.Tensor, idx: torch.Tensor) -> 
     x, cents = _check_pair(x, cents, "sampled_inertia")
     B, N, D = x.shape
     K = cents.shape[1]
-    idx = _ensure_contig(idx, "idx")
+    idx = _gpu_dense("idx", idx)
     if idx.dtype != torch.int32:
         idx = idx.to(torch.int32)
     S = idx.numel()
