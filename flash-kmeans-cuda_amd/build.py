@@ -53,6 +53,7 @@ KERNEL_SOURCES = [
     "update.hip",
     "finalize.hip",
     "quality.hip",
+    "capi_noalloc.hip",
 ]
 HOST_SOURCES = ["capi.cpp"]
 

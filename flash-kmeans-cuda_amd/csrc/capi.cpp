@@ -377,13 +377,14 @@ size_t fkc_kmeans_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,
 
 }  // extern "C"
 
-namespace {
-// fkc_kmeans_lloyd (init == centroids) and fkc_kmeans_lloyd_from.
-int lloyd_impl(const void* x, const void* init, void* centroids,
-               int32_t* cluster_ids, int64_t B, int64_t N, int64_t K,
-               int64_t D, int dtype, int max_iters, float tol, void* workspace,
-               size_t workspace_bytes, fkc_stream_t stream,
-               int32_t* n_iters_dev, int32_t* n_iters_host) {
+namespace fkc {
+// fkc_kmeans_lloyd (init == centroids), fkc_kmeans_lloyd_from and the
+// static-scratch fkc_kmeans_lloyd_noalloc (profile = false: no events).
+int lloyd_run(const void* x, const void* init, void* centroids,
+              int32_t* cluster_ids, int64_t B, int64_t N, int64_t K,
+              int64_t D, int dtype, int max_iters, float tol, void* workspace,
+              size_t workspace_bytes, fkc_stream_t stream,
+              int32_t* n_iters_dev, int32_t* n_iters_host, bool profile) {
   g_err[0] = 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (int rc = shape_ok(B, N, K, D, "kmeans_lloyd")) return rc;
@@ -440,7 +441,8 @@ int lloyd_impl(const void* x, const void* init, void* centroids,
     // and invalidate) an event otherwise implies, which cost ~5 us around
     // each assign.
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    const int period = g_prof.period.load(std::memory_order_relaxed);
+    const int period =
+        profile ? g_prof.period.load(std::memory_order_relaxed) : 0;
     if (period > 0 && it % period == 0) {
       if (hipEventCreateWithFlags(&e0, hipEventDisableSystemFence) != hipSuccess)
         return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: profiling event creation failed");
@@ -502,7 +504,7 @@ int lloyd_impl(const void* x, const void* init, void* centroids,
   }
   return FKC_OK;
 }
-}  // namespace
+}  // namespace fkc
 
 extern "C" {
 
@@ -511,9 +513,9 @@ int fkc_kmeans_lloyd(const void* x, void* centroids, int32_t* cluster_ids,
                      int max_iters, float tol, void* workspace,
                      size_t workspace_bytes, fkc_stream_t stream,
                      int32_t* n_iters_dev, int32_t* n_iters_host) {
-  return lloyd_impl(x, centroids, centroids, cluster_ids, B, N, K, D, dtype,
-                    max_iters, tol, workspace, workspace_bytes, stream,
-                    n_iters_dev, n_iters_host);
+  return lloyd_run(x, centroids, centroids, cluster_ids, B, N, K, D, dtype,
+                   max_iters, tol, workspace, workspace_bytes, stream,
+                   n_iters_dev, n_iters_host, true);
 }
 
 int fkc_kmeans_lloyd_from(const void* x, const void* init_centroids,
@@ -522,9 +524,9 @@ int fkc_kmeans_lloyd_from(const void* x, const void* init_centroids,
                           int max_iters, float tol, void* workspace,
                           size_t workspace_bytes, fkc_stream_t stream,
                           int32_t* n_iters_dev, int32_t* n_iters_host) {
-  return lloyd_impl(x, init_centroids, centroids, cluster_ids, B, N, K, D,
-                    dtype, max_iters, tol, workspace, workspace_bytes, stream,
-                    n_iters_dev, n_iters_host);
+  return lloyd_run(x, init_centroids, centroids, cluster_ids, B, N, K, D,
+                   dtype, max_iters, tol, workspace, workspace_bytes, stream,
+                   n_iters_dev, n_iters_host, true);
 }
 
 void fkc_profile_enable(int enable) {

@@ -162,6 +162,15 @@ int launch_sampled_inertia(const void* x, const void* c, const int32_t* idx,
                            int64_t D, int dtype, double* inertia, void* ws,
                            size_t ws_bytes, hipStream_t s);
 
+// ---------------------------------------------------------------- loop
+// The Lloyd loop behind fkc_kmeans_lloyd*; profile = false ignores the
+// profiling hook (creates no events).
+int lloyd_run(const void* x, const void* init, void* centroids,
+              int32_t* cluster_ids, int64_t B, int64_t N, int64_t K,
+              int64_t D, int dtype, int max_iters, float tol, void* workspace,
+              size_t workspace_bytes, fkc_stream_t stream,
+              int32_t* n_iters_dev, int32_t* n_iters_host, bool profile);
+
 // FKC_NTILES=1|2|4|8: 16-point tiles per wave in the MFMA kernel; 0 = auto.
 int ntiles_override();
 // FKC_KSPLIT=1..64: centroid slices of a sliced MFMA assign; 0 = auto.

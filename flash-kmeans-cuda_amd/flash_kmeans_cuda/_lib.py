@@ -46,6 +46,8 @@ SIGNATURES = {
     "fkc_assigned_inertia": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, _vp, _sz, _vp]),
     "fkc_sampled_inertia_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _int]),
     "fkc_sampled_inertia": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _vp, _vp, _sz, _vp]),
+    "fkc_kmeans_noalloc_max_bytes": (_sz, []),
+    "fkc_kmeans_lloyd_noalloc": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp, _vp, _vp]),
     "fkc_profile_enable": (None, [_int]),
     "fkc_profile_assign_ms": (_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }

@@ -245,6 +245,29 @@ FKC_CAPI int fkc_kmeans_lloyd_from(const void* x, const void* init_centroids,
                                    int32_t* n_iters_host);
 
 /*
+ * fkc_kmeans_lloyd_from without a workspace argument and without any device
+ * allocation: no counterpart in the reference; it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The loop's workspace is a static device array of
+ * fkc_kmeans_noalloc_max_bytes() bytes (64 MiB) that each GPU using the
+ * library holds until the process ends; a shape whose workspace
+ * (fkc_kmeans_workspace_bytes) is larger is refused with FKC_ERR_WORKSPACE.
+ * The array is looked up once per device, on the first call made with that
+ * device current; stream must belong to the current device.  Every call on
+ * one GPU shares the array: calls that overlap on one GPU (other streams or
+ * host threads) race, so serialise them.  Same results as
+ * fkc_kmeans_lloyd_from; the profiling hook is not applied.
+ */
+FKC_CAPI size_t fkc_kmeans_noalloc_max_bytes(void);
+FKC_CAPI int fkc_kmeans_lloyd_noalloc(const void* x, const void* init_centroids,
+                                      void* centroids, int32_t* cluster_ids,
+                                      int64_t B, int64_t N, int64_t K,
+                                      int64_t D, int dtype, int max_iters,
+                                      float tol, fkc_stream_t stream,
+                                      int32_t* n_iters_dev,
+                                      int32_t* n_iters_host);
+
+/*
  * Profiling hook for benchmarks (no counterpart in the reference): with
  * enable = k > 0, fkc_kmeans_lloyd times the assignment launch of every k-th
  * loop iteration (iterations 0, k, 2k, ...) with HIP events stamped by the
