@@ -27,9 +27,11 @@
 // issues under this block's fold).  At the end the four lanes that share a
 // point (l, l+16, l+32, l+48) merge with the lowest-index rule, and the
 // winner's four candidate rows are scored again by the same MFMA chain to
-// pick the first maximal one.  For K <= FKC_EXACT_MAX_K (1024 at D <= 64)
-// the loop tracks the exact index instead (the re-score would cost more than
-// it saves).
+// pick the first maximal one.  For K <= FKC_EXACT_MAX_K (512) the loop
+// tracks the exact index instead (the re-score would cost more than it
+// saves).  Where a launch runs at most two waves per SIMD (grids of <= 512
+// four-tile workgroups at D = 97..128) the loop also keeps each lane's
+// scores of its best block, so no re-score is needed at all.
 // Feature widths that are not a multiple of 32 are zero-padded in registers
 // and LDS (zeros add nothing to a dot product).
 //
@@ -80,7 +82,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define FKC_EXACT_MAX_K 512
 #endif
 #ifndef FKC_EXACT_MAX_K_NARROW
-#define FKC_EXACT_MAX_K_NARROW 1024
+#define FKC_EXACT_MAX_K_NARROW 512
 #endif
 #ifndef FKC_USE_DMA
 #define FKC_USE_DMA 1
@@ -926,11 +928,14 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   p.ds2 = (int)((D + 31) / 32);
   p.pad = D != 32 * p.ds2;
   // Re-scoring the winning block costs about one 16-centroid block per point
-  // tile and a round trip for the candidate rows; below this K the exact
-  // in-loop index is cheaper.  At D <= 64 (fewer MFMAs per block to hide
-  // the fold) up to K = 1024: (8, 65536, 1024, 64) bf16 0.0817 -> 0.0766
-  // ms, (1, 131072, 1024, 64) 0.0282 -> 0.0263 ms; at D = 128 the exact
-  // fold lost at K = 2048 (+8%) and gained 1% at K = 1024.
+  // tile and one round trip for the candidate rows (all of a tile's loads
+  // issued together); below this K the exact in-loop index is cheaper.  The
+  // exact fold costs ~13 vector instructions per four scores against ~5,
+  // which at D <= 64 (two MFMAs per block) makes it vector-ALU-bound: with
+  // the batched re-score the block fold wins from K = 513 at every width
+  // (same labels; (8, 65536, 1024, 64) bf16 0.0884 -> 0.0851 ms,
+  // (1, 262144, 768, 32) 0.0288 -> 0.0238, (4, 100000, 1000, 48) 0.0752 ->
+  // 0.0695).
   p.exact = K <= FKC_EXACT_MAX_K || (p.ds2 <= 2 && K <= FKC_EXACT_MAX_K_NARROW);
   p.pt = choose_pt(p.ds2, p.pad, p.exact, B, N);
   p.S = 1;

@@ -57,6 +57,13 @@ constexpr uint64_t ST_AGG = 1ull << 62;  // the tile's own digit count
 constexpr uint64_t ST_INC = 2ull << 62;  // inclusive prefix over tiles 0..t
 constexpr uint64_t ST_VAL = (1ull << 62) - 1;
 constexpr int SPIN_LIMIT = 1 << 18;  // empty polls per digit walk (< 1 s)
+#ifndef FKC_SORT_LB
+#define FKC_SORT_LB 4
+#endif
+constexpr int LB = FKC_SORT_LB;      // status words read per look-back step
+// Grids of at most this many tiles (per launch) are resident at once, so a
+// tile may take its block index as its place in the chain.
+constexpr int64_t STATIC_TILES_MAX = 256;
 
 struct PassDesc {
   int passes;
@@ -194,7 +201,7 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
                      uint64_t* __restrict__ status,     // this pass, row stride slen
                      int64_t slen, int32_t* __restrict__ tctr,  // this pass, row stride MAXP
                      int32_t* __restrict__ err, int N, int K, int shift,
-                     int bits, int spin_limit,
+                     int bits, int spin_limit, int dyn_tiles,
                      const int32_t* __restrict__ ctrl) {
   constexpr int SW = Geom<TILE>::SW;
   constexpr int PER_WAVE = Geom<TILE>::PER_WAVE;
@@ -215,8 +222,11 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
   // in flight together with the tile-counter atomic.
   const int gc = tid < nb ? gcnt[(size_t)b * MAXP * 256 + tid] : 0;
   for (int i = tid; i < SW * 256; i += ST) (&cnt[0][0])[i] = 0;
+  // Tile index: with dyn_tiles, the order in which workgroups start (a
+  // counter), so every tile a walk waits for is already running; when the
+  // whole grid is resident at once, the block index (one round trip less).
   if (tid == 0) {
-    s_tile = atomicAdd(&tctr[(size_t)b * MAXP], 1);
+    s_tile = dyn_tiles ? atomicAdd(&tctr[(size_t)b * MAXP], 1) : (int)blockIdx.x;
     s_recount = 0;
   }
   __syncthreads();
@@ -276,24 +286,43 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
   if (tid < nb) {
     int64_t excl = 0;
     if (tile > 0) {
+      // The walk reads LB predecessors' status words at once (one round
+      // trip per window instead of one per tile), then takes them newest
+      // first: counts add up until an inclusive prefix; a word not yet
+      // published ends the window, and the walk polls again from it.
       const uint64_t* col = status + (size_t)b * slen + tid;
       int spins = 0;  // one budget for the whole walk
-      for (int t = tile - 1;; --t) {
-        uint64_t v = 0;
-        for (;;) {
-          if (spins >= spin_limit) {
-            stopped = true;
+      int t = tile - 1;
+      for (;;) {
+        if (spins >= spin_limit) {
+          stopped = true;
+          break;
+        }
+        uint64_t v[LB];
+#pragma unroll
+        for (int i = 0; i < LB; ++i)
+          v[i] = t - i >= 0 ? __hip_atomic_load(col + (size_t)(t - i) * 256,
+                                                __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0ull;
+        int used = 0;       // words of the window consumed
+        bool done = false;  // an inclusive prefix (or tile 0) was reached
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+          if (!(v[i] & (ST_AGG | ST_INC))) break;
+          excl += (int64_t)(v[i] & ST_VAL);
+          used = i + 1;
+          if ((v[i] & ST_INC) || t - i == 0) {
+            done = true;
             break;
           }
-          v = __hip_atomic_load(col + (size_t)t * 256, __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
-          if (v & (ST_AGG | ST_INC)) break;
+        }
+        if (done) break;
+        t -= used;
+        if (used < LB) {  // the next word is not published yet
           ++spins;
           __builtin_amdgcn_s_sleep(1);
         }
-        if (stopped) break;
-        excl += (int64_t)(v & ST_VAL);
-        if ((v & ST_INC) || t == 0) break;
       }
       if (stopped)
         s_recount = 1;
@@ -352,9 +381,10 @@ void launch_onesweep(dim3 grid, hipStream_t s, const int32_t* kin,
                      const int32_t* gcnt, uint64_t* status, int64_t slen,
                      int32_t* tctr, int32_t* err, int N, int K, int shift,
                      int bits, int spin_limit, const int32_t* ctrl) {
+  const int dyn = (int64_t)grid.x * grid.y > STATIC_TILES_MAX ? 1 : 0;
   hipLaunchKernelGGL((sort_onesweep_kernel<TILE>), grid, dim3(Geom<TILE>::ST),
                      0, s, kin, vin, kout, vout, gcnt, status, slen, tctr, err,
-                     N, K, shift, bits, spin_limit, ctrl);
+                     N, K, shift, bits, spin_limit, dyn, ctrl);
 }
 
 }  // namespace
