@@ -71,6 +71,11 @@ int save_override() {
   return std::strcmp(s, "1") == 0 ? 1 : (std::strcmp(s, "0") == 0 ? 0 : -1);
 }
 
+bool sort_fuse_override() {
+  const char* s = std::getenv("FKC_SORT_FUSE");
+  return !(s && std::strcmp(s, "0") == 0);
+}
+
 int sort_spin_override(int dflt) {
   const char* s = std::getenv("FKC_SORT_SPIN");
   if (!s || !*s) return dflt;
@@ -467,7 +472,7 @@ int lloyd_run(const void* x, const void* init, void* centroids,
     }
     if (!rc)
       rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
-                             L.sort_ws, L.sort_ws_bytes, ctrl, s, it & 1);
+                             L.sort_ws, L.sort_ws_bytes, ctrl, s, it);
     // The update finalizes the centroids itself when D <= 512 (no sums /
     // counts round trip); otherwise finalize runs as its own kernel.
     const UpdateFinalize fin{centroids, L.c_sq, check ? L.shift + it : nullptr};

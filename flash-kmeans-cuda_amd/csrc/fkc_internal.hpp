@@ -69,13 +69,14 @@ struct SortPlan {
 // the sentinel bin (K = 256 then sorts in one 8-bit pass).
 SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid);
 size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K);
-// phase < 0: standalone call (clears its digit counts first).  phase 0 / 1:
-// the caller alternates phases over consecutive calls on one workspace and
-// cleared it once with label_sort_reset before the first (phase 0) call.
+// seq < 0: standalone call (clears the workspace's control region first).
+// seq >= 0: the number of earlier calls on this workspace since the caller
+// cleared it with label_sort_reset (0, 1, 2, ... over consecutive calls of
+// one shape, each enqueued after the previous one).
 int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
                       int64_t B, int64_t N, int64_t K, bool labels_valid,
                       void* ws, size_t ws_bytes, const int32_t* ctrl,
-                      hipStream_t s, int phase = -1);
+                      hipStream_t s, int64_t seq = -1);
 int label_sort_reset(void* ws, int64_t B, int64_t N, int64_t K, hipStream_t s);
 // The int32 region label_sort_reset zeroes (for fusing it into another
 // launch): *p, *n (n = 0 when B * N == 0).
@@ -83,9 +84,12 @@ void label_sort_reset_region(void* ws, int64_t B, int64_t N, int64_t K,
                              int32_t** p, int64_t* n);
 // FKC_SORT_TILE=256|512|1024|2048|4096: keys per sort tile; 0 = auto.
 int sort_tile_override();
-// FKC_SORT_SPIN=n (n >= 0, tests): look-back spin budget of the sort's tile
-// walks instead of dflt; 0 sends every tile after the first to the recount.
+// FKC_SORT_SPIN=n (n >= 0, tests): spin budget of the sort's waits instead
+// of dflt; 0 sends every wait (look-back walk, row barrier) to its recount.
 int sort_spin_override(int dflt);
+// FKC_SORT_FUSE=0: count digits in a separate upsweep also where the first
+// pass could count them itself (false); otherwise true.
+bool sort_fuse_override();
 
 // ---------------------------------------------------------------- update
 size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D);

@@ -8,41 +8,49 @@
 // caller vouches that every label is valid (labels straight from the assign
 // kernel), split into passes of at most 8 bits.
 //
-// One read of the keys counts the digits of every pass, then each pass is a
-// single kernel that places its tile's keys using a chained scan with
-// decoupled look-back (Merrill & Garland, "Single-pass Parallel Prefix Scan
-// with Decoupled Look-back", 2016; the radix-sort form is Adinets & Merrill,
-// "Onesweep", 2022):
-//   sort_upsweep  : digit histograms of all passes in LDS, added into the
-//                   global per-pass digit counts; also clears the tile
-//                   status words and tile counters the passes will use.
-//   sort_onesweep : a workgroup takes the next tile index from a counter (so
-//                   every tile it waits for is already running), ranks its
-//                   keys stably by digit (per 64-key chunk, one ballot per
-//                   digit bit gives every lane the mask of lanes holding its
-//                   digit, "multi-split"), publishes its per-digit counts,
-//                   then walks back over earlier tiles' status words, adding
-//                   their counts until it meets an inclusive prefix, and
-//                   publishes its own inclusive prefix.  Keys are placed in
-//                   LDS in tile-sorted order and each digit's run is copied
-//                   to its global slot, so writes are runs of consecutive
-//                   addresses.
+// Each pass is a single kernel that places its tile's keys using a chained
+// scan with decoupled look-back (Merrill & Garland, "Single-pass Parallel
+// Prefix Scan with Decoupled Look-back", 2016; the radix-sort form is Adinets
+// & Merrill, "Onesweep", 2022).  A pass needs the row's global digit counts
+// before it places anything:
+//   fused first pass (every tile of the launch resident at once, at most 256
+//                   tiles): each tile adds its digit counts of every pass to
+//                   the row's global counts, then arrives at a row barrier;
+//                   it waits there only after its own look-back, when the
+//                   other tiles have long arrived.
+//   sort_upsweep  : (larger grids) one read of the keys counts the digits of
+//                   every pass into the global counts before the passes.
+//   sort_onesweep : ranks its tile's keys stably by digit (per 64-key chunk,
+//                   one ballot per digit bit gives every lane the mask of
+//                   lanes holding its digit, "multi-split"), publishes its
+//                   per-digit counts, then walks back over earlier tiles'
+//                   status words, adding their counts until it meets an
+//                   inclusive prefix, and publishes its own inclusive prefix.
+//                   Keys are placed in LDS in tile-sorted order and each
+//                   digit's run is copied to its global slot, so writes are
+//                   runs of consecutive addresses.  A resident grid takes the
+//                   block index as the tile's place in the chain; a larger
+//                   one takes the next index from a counter, so every tile a
+//                   walk waits for is already running.
 // A status word is 64 bits: flag in bits 63..62 (published count, or
-// inclusive prefix), count in the rest, read and written with relaxed
-// agent-scope atomics, so a reader sees flag and count together and no fence
-// is needed.  Each wait is bounded: a digit whose walk runs past the spin
-// limit stops waiting, and the workgroup counts that digit's keys in every
-// earlier tile straight from the pass's input (written by the previous
-// launch, so always complete).  That gives the same exclusive prefix as the
-// walk, so the output is correct either way and every workgroup exits; the
-// workspace's first word counts how often the recount ran (zero in a normal
-// run: every tile a walk waits for took its tile index earlier and is
-// already running).
+// inclusive prefix), the call's epoch in bits 61..32, count in bits 31..0,
+// read and written with relaxed agent-scope atomics, so a reader sees flag,
+// epoch and count together and no fence is needed.  A word of an earlier
+// call carries another epoch and reads as unpublished, so status words are
+// never cleared between calls; the tile counters and the barrier's arrival
+// counter only grow, and a call offsets them by its sequence number.
+// Every wait is bounded.  A digit whose walk runs past the spin limit stops
+// waiting, and the workgroup counts that digit's keys in every earlier tile
+// straight from the pass's input (written by the previous launch, so always
+// complete); a tile whose barrier wait runs out counts the whole row's
+// digits itself.  Either gives the same numbers as the wait, so the output
+// is correct either way and every workgroup exits; the workspace's first
+// word counts how often a recount ran (zero in a normal run).
 //
-// The global digit counts accumulate into one of two buffers (the call's
-// phase); the upsweep clears the other, so a caller that alternates phases
-// (the Lloyd loop) clears once per loop, and a standalone call clears its
-// phase-0 buffer first.
+// The global digit counts accumulate into one of two buffers (the parity of
+// the call's sequence number); each call clears the other one, which the
+// previous call used and the next one will.  A standalone call clears the
+// whole control region first.
 // The carried payload is the original index; the last pass writes the
 // user's sorted_ids / perm.
 #include "device_util.hpp"
@@ -55,15 +63,21 @@ constexpr int MAXP = 4;           // passes at most (31-bit keys, 8-bit digits)
 constexpr int UPT = 512;          // threads of the upsweep kernel
 constexpr uint64_t ST_AGG = 1ull << 62;  // the tile's own digit count
 constexpr uint64_t ST_INC = 2ull << 62;  // inclusive prefix over tiles 0..t
-constexpr uint64_t ST_VAL = (1ull << 62) - 1;
-constexpr int SPIN_LIMIT = 1 << 18;  // empty polls per digit walk (< 1 s)
+constexpr uint64_t ST_CNT = 0xffffffffull;  // count field
+constexpr int64_t EPOCHS = (1ll << 30) - 1;  // epochs 1 .. EPOCHS; 0 = cleared
+constexpr int SPIN_LIMIT = 1 << 18;  // empty polls per wait (< 1 s)
 #ifndef FKC_SORT_LB
 #define FKC_SORT_LB 4
 #endif
 constexpr int LB = FKC_SORT_LB;      // status words read per look-back step
 // Grids of at most this many tiles (per launch) are resident at once, so a
-// tile may take its block index as its place in the chain.
+// tile may take its block index as its place in the chain and the first
+// pass may wait at a row barrier.
 constexpr int64_t STATIC_TILES_MAX = 256;
+// Per-row counters (uint64): the tile counter of each pass, then the
+// arrival counter of the fused first pass.
+constexpr int CTR = 8;
+constexpr int CTR_ARRIVE = MAXP;
 
 struct PassDesc {
   int passes;
@@ -86,17 +100,18 @@ __device__ inline uint32_t sort_key(int32_t id, int K) {
   return (uint32_t)id < (uint32_t)K ? (uint32_t)id : (uint32_t)K;
 }
 
-// Workspace layout, shared by the size query and the launcher.
+// Workspace layout, shared by the size query and the launcher.  err, gcnt,
+// ctr and status are consecutive: the control region a reset clears.
 struct SortBufs {
-  int32_t* err;      // [1] recounts after a look-back wait ran out of spins
-  int32_t* gcnt;     // [2 phases][B][MAXP][256] global digit counts; err and
-                     // phase 0 are contiguous (one fill clears both)
-  int32_t* tctr;     // [B][MAXP] tile counters
+  int32_t* err;      // [1] recounts after a wait ran out of spins
+  int32_t* gcnt;     // [2 phases][B][MAXP][256] global digit counts
+  uint64_t* ctr;     // [B][CTR] tile counters, arrival counter
   uint64_t* status;  // [B][P][ntiles][256] tile status words
   int32_t* tk[2];    // ping buffers: keys
   int32_t* tv[2];    //               payload
   int64_t gphase;    // int32 entries per phase of gcnt
   int64_t slen;      // status words per batch row
+  int64_t nctl;      // int32 words of the control region
 };
 
 SortBufs carve_sort(void* ws, int64_t B, int64_t N, int64_t K, size_t* used) {
@@ -106,9 +121,10 @@ SortBufs carve_sort(void* ws, int64_t B, int64_t N, int64_t K, size_t* used) {
   s.gphase = B * MAXP * 256;
   s.err = c.take<int32_t>((size_t)64 + 2 * s.gphase);
   s.gcnt = s.err ? s.err + 64 : nullptr;
-  s.tctr = c.take<int32_t>((size_t)B * MAXP);
+  s.ctr = c.take<uint64_t>((size_t)B * CTR);
   s.slen = (int64_t)p.passes * p.ntiles * 256;
   s.status = c.take<uint64_t>((size_t)B * s.slen);
+  s.nctl = (int64_t)(c.used / sizeof(int32_t));
   const int tmp = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
   for (int i = 0; i < tmp; ++i) {
     s.tk[i] = c.take<int32_t>((size_t)B * N);
@@ -119,34 +135,20 @@ SortBufs carve_sort(void* ws, int64_t B, int64_t N, int64_t K, size_t* used) {
 }
 
 // Digit counts of every pass over this workgroup's keys, added into
-// gcnt_cur; the workgroup also clears its share of the row's status words,
-// and workgroup 0 the row's tile counters and the other phase's counts.
+// gcnt_cur; workgroup 0 of a row also clears the row's other-phase counts.
 __global__ void __launch_bounds__(UPT)
 sort_upsweep_kernel(const int32_t* __restrict__ keys, int N, int K,
                     PassDesc pd, int per_wg, int32_t* __restrict__ gcnt_cur,
                     int32_t* __restrict__ gcnt_next,
-                    uint64_t* __restrict__ status, int64_t slen,
-                    int32_t* __restrict__ tctr,
                     const int32_t* __restrict__ ctrl) {
   if (loop_done(ctrl)) return;
   __shared__ int h[MAXP][256];
   const int tid = threadIdx.x;
-  const int w = blockIdx.x, b = blockIdx.y, U = gridDim.x;
+  const int w = blockIdx.x, b = blockIdx.y;
   for (int i = tid; i < MAXP * 256; i += UPT) (&h[0][0])[i] = 0;
-  {
-    // slen is a multiple of 256, so every share is whole 16-byte pairs.
-    const int64_t per = ((slen + U - 1) / U + 1) / 2 * 2;
-    const int64_t lo = min((int64_t)w * per, slen);
-    const int64_t hi = min(lo + per, slen);
-    uint64_t* sb = status + (size_t)b * slen;
-    for (int64_t i = lo + 2 * tid; i < hi; i += 2 * UPT)
-      *reinterpret_cast<ulonglong2*>(sb + i) = ulonglong2{0ull, 0ull};
-  }
-  if (w == 0) {
+  if (w == 0)
     for (int i = tid; i < MAXP * 256; i += UPT)
       gcnt_next[(size_t)b * MAXP * 256 + i] = 0;
-    if (tid < MAXP) tctr[(size_t)b * MAXP + tid] = 0;
-  }
   __syncthreads();
   const int32_t* kb = keys + (size_t)b * N;
   const int lo = w * per_wg, hi = min(lo + per_wg, N);
@@ -191,49 +193,91 @@ __device__ inline int2 scan256x2(int a, int c, int* wtot, int tid) {
   return int2{ba + ia - a, bc + ic - c};
 }
 
+struct SweepArgs {
+  const int32_t* keys_in;
+  const int32_t* vals_in;  // null: the identity payload (first pass)
+  int32_t* keys_out;
+  int32_t* vals_out;
+  int32_t* gcnt;           // this call's digit counts, row stride MAXP*256
+  int32_t* gnext;          // the other phase (cleared by a fused pass)
+  uint64_t* status;        // this pass's status words, row stride slen
+  int64_t slen;
+  uint64_t* ctr;           // per-row counters, row stride CTR
+  int32_t* err;
+  const int32_t* ctrl;
+  PassDesc pd;
+  int64_t seq;             // sort calls on this workspace since its reset
+  uint64_t tag;            // this call's epoch, in place (bits 61..32)
+  int N, K, pass, spin_limit;
+  int dyn_tiles;           // tile index from the row's counter
+  int fuse;                // first pass that also counts every pass's digits
+};
+
+// Published for this call: flag set and this call's epoch.
+__device__ inline bool st_published(uint64_t v, uint64_t tag) {
+  const uint64_t hi = v & ~ST_CNT;
+  return hi == (ST_AGG | tag) || hi == (ST_INC | tag);
+}
+
 template <int TILE, int ST = Geom<TILE>::ST>
-__global__ void __launch_bounds__(ST)
-sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
-                     const int32_t* __restrict__ vals_in,
-                     int32_t* __restrict__ keys_out,
-                     int32_t* __restrict__ vals_out,
-                     const int32_t* __restrict__ gcnt,  // this pass, row stride MAXP*256
-                     uint64_t* __restrict__ status,     // this pass, row stride slen
-                     int64_t slen, int32_t* __restrict__ tctr,  // this pass, row stride MAXP
-                     int32_t* __restrict__ err, int N, int K, int shift,
-                     int bits, int spin_limit, int dyn_tiles,
-                     const int32_t* __restrict__ ctrl) {
+__global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   constexpr int SW = Geom<TILE>::SW;
   constexpr int PER_WAVE = Geom<TILE>::PER_WAVE;
   constexpr int CHUNKS = Geom<TILE>::CHUNKS;
-  if (loop_done(ctrl)) return;
+  if (loop_done(a.ctrl)) return;
   __shared__ int cnt[SW][256];
+  __shared__ int hx[MAXP - 1][256];  // fused: digit counts of later passes
   __shared__ int gbase[256];
   __shared__ int dstart[256];
   __shared__ int wtot[8];
   __shared__ int s_tile;
   __shared__ int s_recount;  // a digit of this tile stopped waiting
+  __shared__ int s_short;    // the row barrier's wait ran out (fused)
   __shared__ int32_t skey[TILE];
   __shared__ int32_t sval[TILE];
+  const int N = a.N, K = a.K;
+  const int shift = a.pd.shift[a.pass], bits = a.pd.bits[a.pass];
+  const bool fuse = a.fuse != 0;
   const int nb = 1 << bits;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
+  const int64_t ntiles = gridDim.x;
+  int32_t* grow = a.gcnt + (size_t)b * MAXP * 256;
+  uint64_t* crow = a.ctr + (size_t)b * CTR;
+  uint64_t* srow = a.status + (size_t)b * a.slen;
   // The pass's global digit count does not depend on the tile: its load is
-  // in flight together with the tile-counter atomic.
-  const int gc = tid < nb ? gcnt[(size_t)b * MAXP * 256 + tid] : 0;
+  // in flight together with the tile-counter atomic.  (A fused pass has it
+  // only after the row barrier.)
+  int gc = (!fuse && tid < nb) ? grow[a.pass * 256 + tid] : 0;
   for (int i = tid; i < SW * 256; i += ST) (&cnt[0][0])[i] = 0;
-  // Tile index: with dyn_tiles, the order in which workgroups start (a
-  // counter), so every tile a walk waits for is already running; when the
-  // whole grid is resident at once, the block index (one round trip less).
+  if (fuse)
+    for (int i = tid; i < (MAXP - 1) * 256; i += ST) (&hx[0][0])[i] = 0;
+  // Tile index: with dyn_tiles, the order in which workgroups start (the
+  // counter grows by ntiles per call), so every tile a walk waits for is
+  // already running; when the whole grid is resident at once, the block
+  // index (one round trip less).
   if (tid == 0) {
-    s_tile = dyn_tiles ? atomicAdd(&tctr[(size_t)b * MAXP], 1) : (int)blockIdx.x;
+    s_tile = a.dyn_tiles
+                 ? (int)(atomicAdd(reinterpret_cast<unsigned long long*>(
+                                       crow + a.pass),
+                                   1ull) -
+                         (unsigned long long)a.seq * ntiles)
+                 : (int)blockIdx.x;
     s_recount = 0;
+    s_short = 0;
   }
   __syncthreads();
   const int tile = s_tile;
+  // A counter out of step with seq (a caller that broke the sequence
+  // contract) must not send the workgroup outside the row: it leaves, and
+  // the workspace's second word records it.
+  if (tile < 0 || tile >= ntiles) {
+    if (tid == 0) atomicAdd(a.err + 1, 1);
+    return;
+  }
 
-  const int32_t* kb = keys_in + (size_t)b * N;
-  const int32_t* vb = vals_in ? vals_in + (size_t)b * N : nullptr;
+  const int32_t* kb = a.keys_in + (size_t)b * N;
+  const int32_t* vb = a.vals_in ? a.vals_in + (size_t)b * N : nullptr;
   const int tbase = tile * TILE;
   const int tn = min(TILE, N - tbase);  // keys in this tile
   const int base = tbase + wave * PER_WAVE;
@@ -250,7 +294,8 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const bool valid = base + c * 64 + lane < N;
-    const uint32_t d = (sort_key(kk[c], K) >> shift) & dmask;
+    const uint32_t key = sort_key(kk[c], K);
+    const uint32_t d = (key >> shift) & dmask;
     uint64_t match = __builtin_amdgcn_ballot_w64(valid);
     for (int bit = 0; bit < bits; ++bit) {
       const bool on = (d >> bit) & 1u;
@@ -262,11 +307,18 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
     if (valid && below == 0) cnt[wave][d] = old + __popcll(match);
     rank[c] = valid ? old + (int)below : -1;
     dig[c] = (int)d;
+    if (fuse && valid)
+      for (int p = 1; p < a.pd.passes; ++p)
+        atomicAdd(&hx[p - 1][(key >> a.pd.shift[p]) &
+                             ((1u << a.pd.bits[p]) - 1u)],
+                  1);
   }
   __syncthreads();
 
   // Per digit: the waves' offsets inside the digit and the tile's count,
-  // published at once so later tiles can move on.
+  // published at once so later tiles can move on.  A fused pass also adds
+  // the tile's counts of every pass into the row's global counts and makes
+  // them visible before the workgroup arrives at the row barrier.
   int total = 0;
   if (tid < 256) {
     if (tid < nb) {
@@ -275,13 +327,33 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
         cnt[w][tid] = total;
         total += v;
       }
-      __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
-                         (tile == 0 ? ST_INC : ST_AGG) | (uint64_t)total,
+      __hip_atomic_store(srow + (size_t)tile * 256 + tid,
+                         (tile == 0 ? ST_INC : ST_AGG) | a.tag | (uint64_t)total,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (fuse && total) atomicAdd(grow + tid, total);
+    }
+    if (fuse) {
+      for (int p = 1; p < a.pd.passes; ++p) {
+        const int v = hx[p - 1][tid];
+        if (v) atomicAdd(grow + p * 256 + tid, v);
+      }
+      // The adds are agent-scope atomics, performed where every workgroup
+      // reads them; waiting for their completion orders them before the
+      // arrival below (a release fence would also write back this XCD's L2,
+      // which cost ~0.1 us per wave).
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
   }
+  // The first tile of a fused row clears the other phase's counts (used by
+  // the previous call, which has finished, and next by the following call).
+  if (fuse && tile == 0)
+    for (int i = tid; i < MAXP * 256; i += ST)
+      a.gnext[(size_t)b * MAXP * 256 + i] = 0;
   // Tile-local and global exclusive digit prefixes.
   const int2 pre = scan256x2(total, gc, wtot, tid);
+  if (fuse && tid == 0)
+    __hip_atomic_fetch_add(crow + CTR_ARRIVE, 1ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
   bool stopped = false;  // this digit's walk ran out of spins
   if (tid < nb) {
     int64_t excl = 0;
@@ -290,11 +362,11 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
       // trip per window instead of one per tile), then takes them newest
       // first: counts add up until an inclusive prefix; a word not yet
       // published ends the window, and the walk polls again from it.
-      const uint64_t* col = status + (size_t)b * slen + tid;
+      const uint64_t* col = srow + tid;
       int spins = 0;  // one budget for the whole walk
       int t = tile - 1;
       for (;;) {
-        if (spins >= spin_limit) {
+        if (spins >= a.spin_limit) {
           stopped = true;
           break;
         }
@@ -309,8 +381,8 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
         bool done = false;  // an inclusive prefix (or tile 0) was reached
 #pragma unroll
         for (int i = 0; i < LB; ++i) {
-          if (!(v[i] & (ST_AGG | ST_INC))) break;
-          excl += (int64_t)(v[i] & ST_VAL);
+          if (!st_published(v[i], a.tag)) break;
+          excl += (int64_t)(v[i] & ST_CNT);
           used = i + 1;
           if ((v[i] & ST_INC) || t - i == 0) {
             done = true;
@@ -327,12 +399,12 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
       if (stopped)
         s_recount = 1;
       else
-        __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
-                           ST_INC | (uint64_t)(excl + total), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(srow + (size_t)tile * 256 + tid,
+                           ST_INC | a.tag | (uint64_t)(excl + total),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     dstart[tid] = pre.x;
-    gbase[tid] = pre.y + (int)excl - pre.x;
+    gbase[tid] = pre.y + (int)excl - pre.x;  // fused: pre.y == 0 here
   }
   __syncthreads();
   if (s_recount) {  // workgroup-uniform; never taken in a normal run
@@ -347,13 +419,53 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
     __syncthreads();
     if (stopped) {
       const int excl = rc[tid];
-      __hip_atomic_store(status + (size_t)b * slen + (size_t)tile * 256 + tid,
-                         ST_INC | (uint64_t)(excl + total), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(srow + (size_t)tile * 256 + tid,
+                         ST_INC | a.tag | (uint64_t)(excl + total),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       gbase[tid] = pre.y + excl - pre.x;
     }
-    if (tid == 0) atomicAdd(err, 1);
+    if (tid == 0) atomicAdd(a.err, 1);
     __syncthreads();
+  }
+  if (fuse) {  // workgroup-uniform
+    // Row barrier: every tile of the row has added its counts once the
+    // arrival counter reaches ntiles more than before this call.
+    if (tid == 0) {
+      const uint64_t want = (uint64_t)(a.seq + 1) * (uint64_t)ntiles;
+      int spins = 0;
+      int ok = 0;
+      while (spins < a.spin_limit) {
+        if (__hip_atomic_load(crow + CTR_ARRIVE, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT) >= want) {
+          ok = 1;
+          break;
+        }
+        ++spins;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      s_short = !ok;
+    }
+    __syncthreads();
+    if (!s_short) {
+      // Agent-scope atomic loads read the counts where the adds were
+      // performed (no stale cached copy).
+      gc = tid < nb ? __hip_atomic_load(grow + tid, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT)
+                    : 0;
+    } else {
+      // Count the whole row's digits of this pass from its input.
+      int* rc = skey;
+      for (int i = tid; i < 256; i += ST) rc[i] = 0;
+      __syncthreads();
+      for (int n = tid; n < N; n += ST)
+        atomicAdd(&rc[(sort_key(kb[n], K) >> shift) & dmask], 1);
+      __syncthreads();
+      gc = tid < nb ? rc[tid] : 0;
+      if (tid == 0) atomicAdd(a.err, 1);
+      __syncthreads();
+    }
+    const int2 g = scan256x2(gc, 0, wtot, tid);
+    if (tid < nb) gbase[tid] += g.x;
   }
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
@@ -364,8 +476,8 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
     }
   }
   __syncthreads();
-  int32_t* ko = keys_out + (size_t)b * N;
-  int32_t* vo = vals_out + (size_t)b * N;
+  int32_t* ko = a.keys_out + (size_t)b * N;
+  int32_t* vo = a.vals_out + (size_t)b * N;
   for (int i = tid; i < tn; i += ST) {
     const int32_t key = skey[i];
     const int d = (int)((sort_key(key, K) >> shift) & dmask);
@@ -376,15 +488,9 @@ sort_onesweep_kernel(const int32_t* __restrict__ keys_in,
 }
 
 template <int TILE>
-void launch_onesweep(dim3 grid, hipStream_t s, const int32_t* kin,
-                     const int32_t* vin, int32_t* kout, int32_t* vout,
-                     const int32_t* gcnt, uint64_t* status, int64_t slen,
-                     int32_t* tctr, int32_t* err, int N, int K, int shift,
-                     int bits, int spin_limit, const int32_t* ctrl) {
-  const int dyn = (int64_t)grid.x * grid.y > STATIC_TILES_MAX ? 1 : 0;
+void launch_onesweep(dim3 grid, hipStream_t s, const SweepArgs& a) {
   hipLaunchKernelGGL((sort_onesweep_kernel<TILE>), grid, dim3(Geom<TILE>::ST),
-                     0, s, kin, vin, kout, vout, gcnt, status, slen, tctr, err,
-                     N, K, shift, bits, spin_limit, dyn, ctrl);
+                     0, s, a);
 }
 
 }  // namespace
@@ -428,7 +534,7 @@ size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K) {
 int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
                       int64_t B, int64_t N, int64_t K, bool labels_valid,
                       void* ws, size_t ws_bytes, const int32_t* ctrl,
-                      hipStream_t s, int phase) {
+                      hipStream_t s, int64_t seq) {
   if (B == 0 || N == 0) return FKC_OK;
   const size_t need = sort_workspace_bytes(B, N, K);
   if (ws_bytes < need || (need > 0 && ws == nullptr))
@@ -443,69 +549,72 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
     return rc ? rc : launch_iota_i32(perm, B, N, s);
   }
   SortBufs w = carve_sort(ws, B, N, K, nullptr);
-  if (phase < 0) {
-    int rc = launch_fill_i32(w.err, 0, 64 + w.gphase, s);
+  if (seq < 0) {
+    int rc = launch_fill_i32(w.err, 0, w.nctl, s);
     if (rc) return rc;
-    phase = 0;
+    seq = 0;
   }
-  int32_t* gcur = w.gcnt + (size_t)(phase & 1) * w.gphase;
-  int32_t* gnext = w.gcnt + (size_t)((phase & 1) ^ 1) * w.gphase;
+  int32_t* gcur = w.gcnt + (size_t)(seq & 1) * w.gphase;
+  int32_t* gnext = w.gcnt + (size_t)((seq & 1) ^ 1) * w.gphase;
   PassDesc pd{};
   pd.passes = p.passes;
   for (int i = 0; i < p.passes; ++i) {
     pd.bits[i] = p.bits[i];
     pd.shift[i] = p.shift[i];
   }
-  // Upsweep: about 128 workgroups per batch row, 1024..8192 keys each.
-  int per_wg = 1024;
-  while (per_wg < 8192 && (N + per_wg - 1) / per_wg > 128) per_wg <<= 1;
-  const int64_t slen = (int64_t)p.passes * p.ntiles * 256;
-  dim3 ugrid((unsigned)((N + per_wg - 1) / per_wg), (unsigned)B);
-  hipLaunchKernelGGL(sort_upsweep_kernel, ugrid, dim3(UPT), 0, s, ids, (int)N,
-                     (int)K, pd, per_wg, gcur, gnext, w.status, slen, w.tctr,
-                     ctrl);
-  int rc = check_launch("sort_upsweep");
-  if (rc) return rc;
+  // A grid that is resident at once takes block indices as tiles and counts
+  // the digits in its first pass; a larger one needs the upsweep.
+  const bool resident = B * p.ntiles <= STATIC_TILES_MAX;
+  const bool fuse = resident && sort_fuse_override();
+  int rc = FKC_OK;
+  if (!fuse) {
+    // Upsweep: about 128 workgroups per batch row, 1024..8192 keys each.
+    int per_wg = 1024;
+    while (per_wg < 8192 && (N + per_wg - 1) / per_wg > 128) per_wg <<= 1;
+    dim3 ugrid((unsigned)((N + per_wg - 1) / per_wg), (unsigned)B);
+    hipLaunchKernelGGL(sort_upsweep_kernel, ugrid, dim3(UPT), 0, s, ids,
+                       (int)N, (int)K, pd, per_wg, gcur, gnext, ctrl);
+    rc = check_launch("sort_upsweep");
+    if (rc) return rc;
+  }
 
-  // FKC_SORT_SPIN (tests): a smaller look-back spin budget; 0 makes every
-  // tile after the first take the recount path.
-  const int spin = sort_spin_override(SPIN_LIMIT);
-  const int32_t* kin = ids;
-  const int32_t* vin = nullptr;  // identity payload on the first pass
+  SweepArgs a{};
+  a.gcnt = gcur;
+  a.gnext = gnext;
+  a.slen = w.slen;
+  a.ctr = w.ctr;
+  a.err = w.err;
+  a.ctrl = ctrl;
+  a.pd = pd;
+  a.seq = seq;
+  a.tag = (uint64_t)(1 + seq % EPOCHS) << 32;
+  a.N = (int)N;
+  a.K = (int)K;
+  // FKC_SORT_SPIN (tests): a smaller spin budget; 0 sends every wait to its
+  // recount.
+  a.spin_limit = sort_spin_override(SPIN_LIMIT);
+  a.dyn_tiles = resident ? 0 : 1;
+  a.keys_in = ids;
+  a.vals_in = nullptr;  // identity payload on the first pass
   for (int i = 0; i < p.passes; ++i) {
     const bool last = i == p.passes - 1;
-    int32_t* kout = last ? sorted_ids : w.tk[i % 2];
-    int32_t* vout = last ? perm : w.tv[i % 2];
+    a.keys_out = last ? sorted_ids : w.tk[i % 2];
+    a.vals_out = last ? perm : w.tv[i % 2];
+    a.status = w.status + (size_t)i * p.ntiles * 256;
+    a.pass = i;
+    a.fuse = fuse && i == 0 ? 1 : 0;
     dim3 grid((unsigned)p.ntiles, (unsigned)B);
-    const int32_t* gc = gcur + (size_t)i * 256;
-    uint64_t* st = w.status + (size_t)i * p.ntiles * 256;
-    int32_t* tc = w.tctr + i;
     switch (p.tile) {
-      case 256:
-        launch_onesweep<256>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
-        break;
-      case 512:
-        launch_onesweep<512>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                             w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
-        break;
-      case 1024:
-        launch_onesweep<1024>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
-        break;
-      case 2048:
-        launch_onesweep<2048>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
-        break;
-      default:
-        launch_onesweep<4096>(grid, s, kin, vin, kout, vout, gc, st, slen, tc,
-                              w.err, (int)N, (int)K, p.shift[i], p.bits[i], spin, ctrl);
-        break;
+      case 256: launch_onesweep<256>(grid, s, a); break;
+      case 512: launch_onesweep<512>(grid, s, a); break;
+      case 1024: launch_onesweep<1024>(grid, s, a); break;
+      case 2048: launch_onesweep<2048>(grid, s, a); break;
+      default: launch_onesweep<4096>(grid, s, a); break;
     }
     rc = check_launch("sort_onesweep");
     if (rc) return rc;
-    kin = kout;
-    vin = vout;
+    a.keys_in = a.keys_out;
+    a.vals_in = a.vals_out;
   }
   return FKC_OK;
 }
@@ -525,7 +634,7 @@ void label_sort_reset_region(void* ws, int64_t B, int64_t N, int64_t K,
   if (B == 0 || N == 0) return;
   SortBufs w = carve_sort(ws, B, N, K, nullptr);
   *p = w.err;
-  *n = 64 + w.gphase;
+  *n = w.nctl;
 }
 
 }  // namespace fkc

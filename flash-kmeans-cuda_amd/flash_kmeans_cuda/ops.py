@@ -76,8 +76,9 @@ def label_sort(cluster_ids: torch.Tensor, K: int, *,
     Labels outside [0, K) sort after every valid label, in index order.
     workspace: optional caller-owned uint8 CUDA tensor of at least
     fkc_label_sort_workspace_bytes(B, N, K) bytes, 256-byte aligned; after
-    the call its first int32 counts the tiles whose bounded look-back wait ran
-    out and that recounted their prefix instead (a diagnostic: the output is
+    the call its first int32 counts the sort tiles whose bounded wait (on
+    earlier tiles, or at the first pass's row barrier) ran out and that
+    recounted from the pass's input instead (a diagnostic: the output is
     valid either way).
     """
     cluster_ids = _as_i32(_gpu_dense("cluster_ids", cluster_ids))

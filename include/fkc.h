@@ -115,10 +115,11 @@ FKC_CAPI int fkc_row_sqnorm(const void* src, float* out, int64_t rows,
  * Replaces torch.sort(cluster_ids, dim=1) at ops.py:89 (the reference asks
  * stable=False; this sort is always stable).
  * The output is always valid.  Each pass chains its key tiles with bounded
- * waits (decoupled look-back); a tile whose wait runs out recounts its
- * prefix from the pass's input instead, which gives the same result.  The
- * workspace's first int32, cleared by every call, counts those recounts
- * (0 in a normal run; a diagnostic, not an error).
+ * waits (decoupled look-back, and a row barrier where the first pass counts
+ * the digits); a tile whose wait runs out recounts what it waited for from
+ * the pass's input instead, which gives the same result.  The workspace's
+ * first int32, cleared by every call, counts those recounts (0 in a normal
+ * run; a diagnostic, not an error).
  */
 FKC_CAPI size_t fkc_label_sort_workspace_bytes(int64_t B, int64_t N,
                                                int64_t K);

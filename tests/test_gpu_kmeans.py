@@ -209,18 +209,26 @@ def test_tol_stops_at_the_oracles_iteration():
     assert torch.equal(it, _T(init, "bf16")), "init_centroids was modified"
 
 
-def test_loop_with_sort_recounts(monkeypatch):
-    """With a zero look-back spin budget every sort tile after the first
-    recounts its prefix from the pass's input; the Lloyd loop's result is
-    the same bits as with the normal look-back."""
+@pytest.mark.parametrize("cfg_name,N", [("c3", 65536), ("c2", 32768), ("c4", 8192)])
+def test_loop_sort_paths_agree(monkeypatch, cfg_name, N):
+    """The Lloyd loop gives the same bits whichever way its sorts count
+    digits (in the first pass, or in a separate upsweep: FKC_SORT_FUSE=0)
+    and when every wait of every sort gives up at once (FKC_SORT_SPIN=0:
+    each tile recounts from the pass's input instead of waiting).  Several
+    iterations on one workspace also exercise the status words' epochs."""
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
-    cfg = synth.CONFIGS["c3"]
-    x, init = synth.make(cfg, N=65536)
-    xt, it = _T(x, "f16"), _T(init, "f16")
-    a = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
-    monkeypatch.setenv("FKC_SORT_SPIN", "0")
-    b = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
-    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    cfg = synth.CONFIGS[cfg_name]
+    x, init = synth.make(cfg, N=N)
+    xt, it = _T(x, cfg.dtype), _T(init, cfg.dtype)
+    a = batch_kmeans_Euclid(xt, cfg.K, max_iters=4, init_centroids=it)
+    for fuse, spin in [("0", None), ("1", "0"), ("0", "0")]:
+        monkeypatch.setenv("FKC_SORT_FUSE", fuse)
+        if spin is None:
+            monkeypatch.delenv("FKC_SORT_SPIN", raising=False)
+        else:
+            monkeypatch.setenv("FKC_SORT_SPIN", spin)
+        b = batch_kmeans_Euclid(xt, cfg.K, max_iters=4, init_centroids=it)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), (fuse, spin)
 
 
 def test_verbose_path_equals_fused_loop(capsys):

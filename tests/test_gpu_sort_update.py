@@ -48,8 +48,12 @@ def _sort_ws(B, N, K):
 
 
 def _health(ws):
+    """Word 0 of the workspace (recounts); word 1 (tiles whose counter was
+    out of step with the call sequence) must stay 0."""
     torch.cuda.synchronize()
-    return int(ws[:4].view(torch.int32).item())
+    w = ws[:8].view(torch.int32).cpu()
+    assert int(w[1]) == 0, "sort tile counter out of step"
+    return int(w[0])
 
 
 @pytest.mark.parametrize("B,N,K", SORT_CASES)
@@ -240,16 +244,23 @@ def test_finalize_in_place():
     assert np.array_equal(_np(t, "f16"), O.finalize(sums, counts, old, "f16"))
 
 
+@pytest.mark.parametrize("fuse", [True, False])
 @pytest.mark.parametrize("B,N,K,tile", [(1, 100000, 8192, 4096), (2, 70001, 70000, 1024),
-                                        (1, 524288, 8192, 4096), (3, 9000, 300, 256)])
-def test_label_sort_recount_path(monkeypatch, B, N, K, tile):
-    """With a zero look-back spin budget (FKC_SORT_SPIN=0) every tile after
-    the first stops waiting and recounts its prefix from the pass's input:
-    the output is still the stable sort, bit for bit, and the workspace's
-    first word counts the recounts (one per such tile and pass)."""
+                                        (1, 524288, 8192, 4096), (3, 9000, 300, 256),
+                                        (2, 300000, 1000, 1024)])
+def test_label_sort_recount_path(monkeypatch, B, N, K, tile, fuse):
+    """With a zero spin budget (FKC_SORT_SPIN=0) every wait gives up at
+    once: each tile after the first recounts its prefix from the pass's
+    input, and where the first pass counts the digits itself (every tile
+    resident, at most 256; FKC_SORT_FUSE=0 sends the count to the separate
+    upsweep instead) each tile also counts the whole row's digits rather than
+    wait at the row barrier.  The output is still the stable sort, bit for
+    bit, and the workspace's first word counts the recounts: one per such
+    tile and pass, plus one per tile of a fused first pass."""
     from flash_kmeans_cuda.ops import label_sort
     monkeypatch.setenv("FKC_SORT_TILE", str(tile))
     monkeypatch.setenv("FKC_SORT_SPIN", "0")
+    monkeypatch.setenv("FKC_SORT_FUSE", "1" if fuse else "0")
     rng = np.random.default_rng(N + tile)
     ids = rng.integers(-1, K + 1, (B, N)).astype(np.int32)
     ws = _sort_ws(B, N, K)
@@ -259,7 +270,8 @@ def test_label_sort_recount_path(monkeypatch, B, N, K, tile):
     ntiles = (N + tile - 1) // tile
     bits = int(np.ceil(np.log2(K + 1)))
     passes = (bits + 7) // 8
-    assert _health(ws) == B * passes * (ntiles - 1)
+    fused = fuse and B * ntiles <= 256
+    assert _health(ws) == B * passes * (ntiles - 1) + (B * ntiles if fused else 0)
     monkeypatch.delenv("FKC_SORT_SPIN")
     s2, p2 = label_sort(_t(ids), K, workspace=ws)
     assert torch.equal(s2, s) and torch.equal(p2, p) and _health(ws) == 0
