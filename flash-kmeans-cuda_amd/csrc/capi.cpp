@@ -426,12 +426,13 @@ int lloyd_run(const void* x, const void* init, void* centroids,
   const bool check = tol > 0.f;
   const int32_t* ctrl = check ? L.ctrl : nullptr;
   // One prologue launch: copy of the initial centroids (when separate),
-  // their c_sq, and the zeroing of the control words, the sort's first
-  // phase and the shift slots.
+  // their c_sq, and the zeroing of the control words, the sort's and the
+  // update's control regions and the shift slots.
   ZeroFill zf;
   zf.z0 = L.ctrl;
   zf.n0 = 4;
   label_sort_reset_region(L.sort_ws, B, N, K, &zf.z1, &zf.n1);
+  update_control_region(L.upd_ws, B, N, D, &zf.z3, &zf.n3);
   if (check) {
     zf.z2 = L.shift;
     zf.n2 = max_iters;
@@ -480,7 +481,7 @@ int lloyd_run(const void* x, const void* init, void* centroids,
     if (!rc)
       rc = launch_update(x, L.perm, L.sorted, L.sums, L.counts, B, N, K, D,
                          dtype, true, L.upd_ws, L.upd_ws_bytes, ctrl, s, &fin,
-                         &fused);
+                         &fused, it);
     if (!rc && !fused)
       rc = launch_finalize(L.sums, L.counts, centroids, centroids, L.c_sq,
                            check ? L.shift + it : nullptr, B, K, D, dtype, ctrl,

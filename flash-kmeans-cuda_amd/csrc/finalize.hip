@@ -89,8 +89,8 @@ __global__ void iota_i32_kernel(int32_t* p, int64_t B, int64_t N) {
 // per row) copy the initial centroids into the loop's centroid buffer when
 // the two differ and write their squared norms with the column order and
 // wave reduction of row_sqnorm_kernel (the same bits); the blocks after
-// them zero the loop's control words, the label sort's error word and
-// first digit counts and, with a tolerance, the shift slots.
+// them zero the loop's control words, the label sort's and the update's
+// control regions and, with a tolerance, the shift slots.
 template <int DT>
 __global__ void __launch_bounds__(256)
 lloyd_prologue_kernel(const typename Elem<DT>::T* __restrict__ init,
@@ -98,7 +98,8 @@ lloyd_prologue_kernel(const typename Elem<DT>::T* __restrict__ init,
                       float* __restrict__ c_sq, int64_t rows, int D,
                       int32_t* __restrict__ z0, int64_t n0,
                       int32_t* __restrict__ z1, int64_t n1,
-                      float* __restrict__ z2, int64_t n2) {
+                      float* __restrict__ z2, int64_t n2,
+                      int32_t* __restrict__ z3, int64_t n3) {
   using E = Elem<DT>;
   const int64_t row_blocks = (rows + 3) / 4;
   if ((int64_t)blockIdx.x >= row_blocks) {
@@ -107,6 +108,7 @@ lloyd_prologue_kernel(const typename Elem<DT>::T* __restrict__ init,
     for (int64_t i = i0; i < n0; i += stride) z0[i] = 0;
     for (int64_t i = i0; i < n1; i += stride) z1[i] = 0;
     for (int64_t i = i0; i < n2; i += stride) z2[i] = 0.f;
+    for (int64_t i = i0; i < n3; i += stride) z3[i] = 0;
     return;
   }
   const int lane = threadIdx.x & 63;
@@ -182,15 +184,17 @@ template <int DT>
 int launch_prologue_t(const void* init, void* cent, float* c_sq, int64_t rows,
                       int64_t D, const ZeroFill& f, hipStream_t s) {
   using T = typename Elem<DT>::T;
-  const int64_t nz = f.n0 > f.n1 ? (f.n0 > f.n2 ? f.n0 : f.n2)
-                                 : (f.n1 > f.n2 ? f.n1 : f.n2);
+  int64_t nz = f.n0;
+  if (f.n1 > nz) nz = f.n1;
+  if (f.n2 > nz) nz = f.n2;
+  if (f.n3 > nz) nz = f.n3;
   const int64_t zb = nz > 0 ? (nz + 255) / 256 < 64 ? (nz + 255) / 256 : 64 : 0;
   const int64_t blocks = (rows + 3) / 4 + zb;
   if (blocks <= 0) return FKC_OK;
   hipLaunchKernelGGL((lloyd_prologue_kernel<DT>), dim3((unsigned)blocks),
                      dim3(256), 0, s, static_cast<const T*>(init),
                      static_cast<T*>(cent), c_sq, rows, (int)D, f.z0, f.n0,
-                     f.z1, f.n1, f.z2, f.n2);
+                     f.z1, f.n1, f.z2, f.n2, f.z3, f.n3);
   return check_launch("lloyd_prologue");
 }
 

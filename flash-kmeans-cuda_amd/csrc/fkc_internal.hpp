@@ -107,12 +107,22 @@ struct UpdateFinalize {
 };
 // fin: optional fused finalize; *fused (may be null) reports whether it was
 // applied (it needs D <= 512); when not, the caller runs launch_finalize.
+// seq >= 0 (overwrite mode only): the number of earlier calls on this
+// workspace since the caller cleared its control region
+// (update_control_region), over consecutive calls of one shape, each
+// enqueued after the previous one; block partials are then computed inside
+// the run kernel.  seq < 0: standalone.
 int launch_update(const void* x, const int32_t* perm /*nullable*/,
                   const int32_t* ids_sorted, float* sums, int32_t* counts,
                   int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
                   bool overwrite, void* ws, size_t ws_bytes,
                   const int32_t* ctrl, hipStream_t s,
-                  const UpdateFinalize* fin = nullptr, bool* fused = nullptr);
+                  const UpdateFinalize* fin = nullptr, bool* fused = nullptr,
+                  int64_t seq = -1);
+// The int32 region of an update workspace that a sequenced caller zeroes
+// before its first call: *p, *n (n = 0 when B * N == 0).
+void update_control_region(void* ws, int64_t B, int64_t N, int64_t D,
+                           int32_t** p, int64_t* n);
 
 // ---------------------------------------------------------------- finalize
 // c_sq_out / shift_out may be null.  shift_out receives max over rows of
@@ -132,6 +142,8 @@ struct ZeroFill {
   int64_t n1 = 0;
   float* z2 = nullptr;
   int64_t n2 = 0;
+  int32_t* z3 = nullptr;
+  int64_t n3 = 0;
 };
 // One launch: cent = init (when the pointers differ), c_sq = row squared
 // norms of init (the bits of launch_row_sqnorm), and the zero-fills.

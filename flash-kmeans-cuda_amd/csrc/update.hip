@@ -23,7 +23,10 @@
 //   update_blocks: a run can span many units (few clusters, many points).
 //                  For every block of 64 units that lies wholly inside one
 //                  run, one wave adds the block's 64 head partials in unit
-//                  order into a block partial.
+//                  order into a block partial.  In the Lloyd loop this is
+//                  done inside update_runs instead: the last of a block's
+//                  64 through-units to finish (an arrival counter) sums the
+//                  block, with the same order and bits.
 //   update_merge : the unit where a multi-unit run starts owns it.  It finds
 //                  the run's last unit by ballots over unit and block flags,
 //                  then adds, in unit order, its tail partial, the heads of
@@ -126,6 +129,16 @@ struct UnitMeta {  // per unit, int32 x 4
   enum { TAIL_ID = 0, TAIL_LEN = 1, HEAD_LEN = 2, THROUGH = 3 };
 };
 
+// Block partials computed inside update_runs (null ctr: update_blocks
+// computes them).  Flags of full blocks are set to tag.
+struct BlockArgs {
+  float* part;    // [B][nblocks][D]
+  int32_t* meta;  // [B][nblocks][2]: flag, row count
+  int32_t* ctr;   // [B][nblocks][column blocks] arrival counters
+  int nblocks;
+  int tag;
+};
+
 constexpr int FIN_DMAX = 512;  // widest row the fused finalize handles
 
 // Finalize fused into the update (the Lloyd loop): where a bin's final sum
@@ -192,6 +205,82 @@ __device__ inline void finalize_row(const float* row, int cnt,
   finish_norms(sq, sh, csq, shift, lane);
 }
 
+// Wave-cooperative ordered sum of partial rows (D fp32 each):
+//   out[c] = first[c] + row(0)[c] + ... + row(n-1)[c]   (first may be null)
+// for the columns c in [c_lo, c_hi).  The wave splits into G lane groups;
+// group g sums rows i = g, g+G, g+2G ... in increasing i (eight loads in
+// flight per lane before their adds) over V-wide column vectors, then the
+// group sums are added in group order.  The bracketing depends only on n,
+// so the result is reproducible bit for bit (and a column's bits do not
+// depend on the range it is summed in).  Mode 0 stores out, mode 1 adds
+// into it atomically.  COHERENT reads the rows with agent-scope atomic
+// loads: rows another workgroup of the same launch stored with agent-scope
+// atomic stores.
+template <int V, bool COHERENT>
+__device__ inline void ld_cols(const float* p, float* o) {
+  if constexpr (COHERENT) {
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      o[v] = __hip_atomic_load(p + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if constexpr (V == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else {
+    o[0] = p[0];
+  }
+}
+
+template <int V, bool COHERENT = false, typename RowFn>
+__device__ inline void wave_ordered_sum(const float* first, int n, int c_lo,
+                                        int c_hi, RowFn row, float* out,
+                                        int add, int lane) {
+  constexpr int G = 4, LG = 64 / G, PF = 8;
+  const int g = lane / LG, sub = lane % LG;
+  for (int c0 = c_lo; c0 < c_hi; c0 += LG * V) {
+    const int c = c0 + sub * V;
+    const bool cok = c < c_hi;  // (c_hi - c_lo) % V == 0: whole vectors
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.f;
+    if (first != nullptr && g == 0 && cok) ld_cols<V, false>(first + c, acc);
+    for (int i0 = g; i0 < n; i0 += G * PF) {
+      float t[PF][V];
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        const int i = i0 + j * G;
+        if (cok && i < n) {
+          ld_cols<V, COHERENT>(row(i) + c, t[j]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v) t[j][v] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < PF; ++j)
+        if (i0 + j * G < n) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[v] += t[j][v];
+        }
+    }
+    float tot[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) tot[v] = __shfl(acc[v], sub, 64);
+#pragma unroll
+    for (int gg = 1; gg < G; ++gg)
+#pragma unroll
+      for (int v = 0; v < V; ++v) tot[v] += __shfl(acc[v], gg * LG + sub, 64);
+    if (g == 0 && cok) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if (add)
+          unsafeAtomicAdd(out + c + v, tot[v]);
+        else
+          out[c + v] = tot[v];
+      }
+    }
+  }
+}
+
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Wpass-failed"
 template <int DT, int VEC, int NI, bool INDEXED>
@@ -201,7 +290,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
                    const int32_t* __restrict__ sids, float* __restrict__ sums,
                    int32_t* __restrict__ counts, float* __restrict__ part,
                    int32_t* __restrict__ meta, int N, int K, int D,
-                   int nunits, int ur, int overwrite,
+                   int nunits, int ur, int overwrite, BlockArgs blk,
                    FinArgs<typename Elem<DT>::T> fin,
                    const int32_t* __restrict__ ctrl) {
   using T = typename Elem<DT>::T;
@@ -233,6 +322,14 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   const bool has_prev = p0 > 0, has_next = p1 < N;
   const int prev = has_prev ? ib[p0 - 1] : 0;
   const int next = has_next ? ib[p1] : 0;
+  // Block partials in this launch: labels are sorted, so the unit's block
+  // of UB units lies wholly inside one run exactly when the label before
+  // its first row equals the label after its last row.
+  bool bfull = false;  // wave-uniform
+  if (blk.ctr != nullptr) {
+    const int64_t bs = (int64_t)(u / UB) * UB * ur, be = bs + (int64_t)UB * ur;
+    bfull = bs > 0 && be < N && ib[bs - 1] == ib[be];
+  }
 
   int col[NI];
   bool cok[NI];
@@ -264,13 +361,21 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
       for (int k = lo + lane; k < hi; k += 64) cntb[k] = 0;
   };
 
-  auto store_part = [&](int slot, const Acc& a) {
+  // coherent: agent-scope atomic stores, which another workgroup of this
+  // launch may read (the block sum below).
+  auto store_part = [&](int slot, const Acc& a, bool coherent) {
     float* dst = partb + ((size_t)u * 2 + slot) * D;
 #pragma unroll
     for (int i = 0; i < NI; ++i)
       if (cok[i]) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) dst[col[i] + v] = a[i][v];
+        for (int v = 0; v < VEC; ++v) {
+          if (coherent)
+            __hip_atomic_store(dst + col[i] + v, a[i][v], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          else
+            dst[col[i] + v] = a[i][v];
+        }
       }
   };
 
@@ -279,11 +384,11 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     const bool continuing = s == p0 && has_prev && prev == id;
     const bool continued = e == p1 && has_next && next == id;
     if (continuing) {
-      store_part(0, a);
+      store_part(0, a, bfull);
       head_len = e - s;
       through = continued ? 1 : 0;
     } else if (continued) {
-      store_part(1, a);
+      store_part(1, a, false);
       tail_id = id;
       tail_len = e - s;
     } else if (fused && (uint32_t)id < (uint32_t)K) {
@@ -490,85 +595,52 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     m[UnitMeta::HEAD_LEN] = head_len;
     m[UnitMeta::THROUGH] = through;
   }
+
+  // Block partials in this launch (the Lloyd loop): every unit of a block
+  // that lies wholly inside one run arrives at the block's counter (one per
+  // column block) once its head partial is stored; the UB-th arrival sums
+  // the block's head partials, in the order and bracketing of
+  // update_blocks_kernel, into the block partial.  Other blocks are not
+  // touched; their flags keep an earlier tag.
+  if (bfull) {
+    // The head partial's atomic stores are performed where the summing
+    // wave reads them; waiting for them orders them before the arrival.
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int beta = u / UB;
+    int old = 0;
+    if (lane == 0)
+      old = atomicAdd(blk.ctr + ((size_t)b * blk.nblocks + beta) * gridDim.z +
+                          blockIdx.z,
+                      1);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old == UB - 1) {
+      const int c_hi = min(cbase + 64 * VEC * NI, D);
+      float* dst = blk.part + ((size_t)b * blk.nblocks + beta) * D;
+      auto row = [&](int i) {
+        return partb + ((size_t)(beta * UB + i) * 2 + 0) * D;
+      };
+      if (D % 4 == 0)
+        wave_ordered_sum<4, true>(nullptr, UB, cbase, c_hi, row, dst, 0, lane);
+      else
+        wave_ordered_sum<1, true>(nullptr, UB, cbase, c_hi, row, dst, 0, lane);
+      if (lead && lane == 0) {
+        int32_t* bm = blk.meta + ((size_t)b * blk.nblocks + beta) * 2;
+        bm[0] = blk.tag;
+        bm[1] = UB * ur;
+      }
+    }
+  }
 }
 #pragma clang diagnostic pop
 
-// Wave-cooperative ordered sum of partial rows (D fp32 each):
-//   out[c] = first[c] + row(0)[c] + ... + row(n-1)[c]   (first may be null)
-// The wave splits into G lane groups; group g sums rows i = g, g+G, g+2G ...
-// in increasing i (eight loads in flight per lane before their adds) over
-// V-wide column vectors, then the group sums are added in group order.  The
-// bracketing depends only on n, so the result is reproducible bit for bit.
-// Mode 0 stores out, mode 1 adds into it atomically.
-template <int V>
-__device__ inline void ld_cols(const float* p, float* o) {
-  if constexpr (V == 4) {
-    const float4 v = *reinterpret_cast<const float4*>(p);
-    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-  } else {
-    o[0] = p[0];
-  }
-}
-
-template <int V, typename RowFn>
-__device__ inline void wave_ordered_sum(const float* first, int n, int D,
-                                        RowFn row, float* out, int add,
-                                        int lane) {
-  constexpr int G = 4, LG = 64 / G, PF = 8;
-  const int g = lane / LG, sub = lane % LG;
-  for (int c0 = 0; c0 < D; c0 += LG * V) {
-    const int c = c0 + sub * V;
-    const bool cok = c < D;  // D % V == 0: the whole vector is in range
-    float acc[V];
-#pragma unroll
-    for (int v = 0; v < V; ++v) acc[v] = 0.f;
-    if (first != nullptr && g == 0 && cok) ld_cols<V>(first + c, acc);
-    for (int i0 = g; i0 < n; i0 += G * PF) {
-      float t[PF][V];
-#pragma unroll
-      for (int j = 0; j < PF; ++j) {
-        const int i = i0 + j * G;
-        if (cok && i < n) {
-          ld_cols<V>(row(i) + c, t[j]);
-        } else {
-#pragma unroll
-          for (int v = 0; v < V; ++v) t[j][v] = 0.f;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < PF; ++j)
-        if (i0 + j * G < n) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) acc[v] += t[j][v];
-        }
-    }
-    float tot[V];
-#pragma unroll
-    for (int v = 0; v < V; ++v) tot[v] = __shfl(acc[v], sub, 64);
-#pragma unroll
-    for (int gg = 1; gg < G; ++gg)
-#pragma unroll
-      for (int v = 0; v < V; ++v) tot[v] += __shfl(acc[v], gg * LG + sub, 64);
-    if (g == 0 && cok) {
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        if (add)
-          unsafeAtomicAdd(out + c + v, tot[v]);
-        else
-          out[c + v] = tot[v];
-      }
-    }
-  }
-}
-
 // One wave per block of UB units.  A block whose every unit lies inside a
 // single run ("full") gets the ordered sum of its head partials and its row
-// count; other blocks are flagged not full.
+// count, and its flag word is set to `tag`; other blocks get flag 0.
 __global__ void __launch_bounds__(UT)
 update_blocks_kernel(const float* __restrict__ part,
                      const int32_t* __restrict__ meta,
                      float* __restrict__ bpart, int32_t* __restrict__ bmeta,
-                     int D, int nunits, int nblocks,
+                     int D, int nunits, int nblocks, int tag,
                      const int32_t* __restrict__ ctrl) {
   if (loop_done(ctrl)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -594,11 +666,11 @@ update_blocks_kernel(const float* __restrict__ part,
   const int v0 = beta * UB;
   auto row = [&](int i) { return pb + ((size_t)(v0 + i) * 2 + 0) * D; };
   if (D % 4 == 0)
-    wave_ordered_sum<4>(nullptr, UB, D, row, dst, 0, lane);
+    wave_ordered_sum<4>(nullptr, UB, 0, D, row, dst, 0, lane);
   else
-    wave_ordered_sum<1>(nullptr, UB, D, row, dst, 0, lane);
+    wave_ordered_sum<1>(nullptr, UB, 0, D, row, dst, 0, lane);
   if (lane == 0) {
-    bm[0] = 1;
+    bm[0] = tag;
     bm[1] = len;
   }
 }
@@ -611,7 +683,8 @@ update_merge_kernel(const float* __restrict__ part,
                     const float* __restrict__ bpart,
                     const int32_t* __restrict__ bmeta, float* __restrict__ sums,
                     int32_t* __restrict__ counts, int K, int D, int nunits,
-                    int nblocks, int overwrite,
+                    int nblocks, int overwrite, int tag,
+                    int32_t* __restrict__ bctr, int nz,
                     FinArgs<typename Elem<DT>::T> fin,
                     const int32_t* __restrict__ ctrl) {
   __shared__ float fin_row[UT / 64][FIN_DMAX];
@@ -620,6 +693,11 @@ update_merge_kernel(const float* __restrict__ part,
   const int b = blockIdx.y;
   const int u = blockIdx.x * (UT / 64) + wave;
   if (u >= nunits) return;
+  // The first unit of each block clears the block's arrival counters for
+  // the next launch of update_runs (nothing in this launch reads them).
+  if (bctr != nullptr && u % UB == 0)
+    for (int z = lane; z < nz; z += 64)
+      bctr[((size_t)b * nblocks + u / UB) * nz + z] = 0;
   const int32_t* mb = meta + (size_t)b * nunits * 4;
   // Lane j loads the whole record of unit u + j (one 16-byte load): lane 0
   // gives the tail, lanes 1.. the continuation flags and head lengths of the
@@ -655,7 +733,7 @@ update_merge_kernel(const float* __restrict__ part,
       int be = -1;
       for (int b0 = beta0; be < 0 && b0 < nblocks; b0 += 64) {
         const int bb = b0 + lane;
-        const bool nf = bb < nblocks && bmb[(size_t)bb * 2] == 0;
+        const bool nf = bb < nblocks && bmb[(size_t)bb * 2] != tag;
         const uint64_t mm = __builtin_amdgcn_ballot_w64(nf);
         if (mm) be = b0 + (int)__builtin_ctzll(mm);
       }
@@ -693,9 +771,9 @@ update_merge_kernel(const float* __restrict__ part,
   const float* tail = pb + ((size_t)u * 2 + 1) * D;
   const int add = (overwrite || fused) ? 0 : 1;
   if (D % 4 == 0)
-    wave_ordered_sum<4>(tail, n, D, row, dst, add, lane);
+    wave_ordered_sum<4>(tail, n, 0, D, row, dst, add, lane);
   else
-    wave_ordered_sum<1>(tail, n, D, row, dst, add, lane);
+    wave_ordered_sum<1>(tail, n, 0, D, row, dst, add, lane);
   if (fused) {
     wave_lds_sync();
     finalize_row<DT>(fin_row[wave], len, fin.cent + ((size_t)b * K + id) * D,
@@ -711,14 +789,6 @@ update_merge_kernel(const float* __restrict__ part,
   }
 }
 
-struct UpdateBufs {
-  float* part;
-  int32_t* meta;
-  float* bpart;
-  int32_t* bmeta;
-  int64_t nunits, nblocks;
-};
-
 // Column slices per lane pass: VEC columns per lane (2 when D is even), NI
 // slices of 64 lanes per row (1, 2 or 4), and grid.z column blocks beyond.
 inline int runs_vec(int64_t D) { return D % 2 == 0 ? 2 : 1; }
@@ -726,22 +796,55 @@ inline int runs_ni(int64_t D) {
   const int64_t slices = (D + 64 * runs_vec(D) - 1) / (64 * runs_vec(D));
   return slices <= 1 ? 1 : (slices <= 2 ? 2 : 4);
 }
+inline int64_t runs_zblocks(int64_t D) {
+  const int64_t cols = 64 * runs_vec(D) * runs_ni(D);
+  return (D + cols - 1) / cols;
+}
+
+// Workspace layout, shared by the size query and the launcher.  bmeta and
+// bctr are consecutive: the control region the Lloyd loop clears once.
+struct UpdateBufs {
+  float* part;      // [B][nunits][2][D] unit head / tail partials
+  int32_t* meta;    // [B][nunits][4] unit records
+  float* bpart;     // [B][nblocks][D] block partials
+  int32_t* bmeta;   // [B][nblocks][2] block flag, row count
+  int32_t* bctr;    // [B][nblocks][nz] arrival counters
+  int64_t nunits, nblocks, nz;
+  int64_t nctl;     // int32 words from bmeta to the end of bctr
+  size_t used;
+};
+
+UpdateBufs carve_update(void* ws, int64_t B, int64_t N, int64_t D) {
+  const int ur = choose_ur(B, N);
+  UpdateBufs w{};
+  w.nunits = (N + ur - 1) / ur;
+  w.nblocks = (w.nunits + UB - 1) / UB;
+  w.nz = runs_zblocks(D);
+  Carve c(ws);
+  w.part = c.take<float>((size_t)B * w.nunits * 2 * D);
+  w.meta = c.take<int32_t>((size_t)B * w.nunits * 4);
+  w.bpart = c.take<float>((size_t)B * w.nblocks * D);
+  const size_t ctl0 = c.used;
+  w.bmeta = c.take<int32_t>((size_t)B * w.nblocks * 2);
+  w.bctr = c.take<int32_t>((size_t)B * w.nblocks * w.nz);
+  w.nctl = (int64_t)((c.used - ctl0) / sizeof(int32_t));
+  w.used = c.used;
+  return w;
+}
 
 template <int DT, int VEC, int NI, bool INDEXED>
 int launch_runs_t(const void* x, const int32_t* perm, const int32_t* sids,
                   float* sums, int32_t* counts, const UpdateBufs& w, int64_t B,
                   int64_t N, int64_t K, int64_t D, bool overwrite,
-                  FinArgs<typename Elem<DT>::T> fin, const int32_t* ctrl,
-                  hipStream_t s) {
+                  const BlockArgs& blk, FinArgs<typename Elem<DT>::T> fin,
+                  const int32_t* ctrl, hipStream_t s) {
   using T = typename Elem<DT>::T;
   const int ur = choose_ur(B, N);
-  const int64_t cols_per_block = 64 * VEC * NI;
-  dim3 grid((unsigned)((w.nunits + 3) / 4), (unsigned)B,
-            (unsigned)((D + cols_per_block - 1) / cols_per_block));
+  dim3 grid((unsigned)((w.nunits + 3) / 4), (unsigned)B, (unsigned)w.nz);
   hipLaunchKernelGGL((update_runs_kernel<DT, VEC, NI, INDEXED>), grid,
                      dim3(UT), 0, s, static_cast<const T*>(x), perm, sids,
                      sums, counts, w.part, w.meta, (int)N, (int)K, (int)D,
-                     (int)w.nunits, ur, overwrite ? 1 : 0, fin, ctrl);
+                     (int)w.nunits, ur, overwrite ? 1 : 0, blk, fin, ctrl);
   return check_launch("update_runs");
 }
 
@@ -749,12 +852,12 @@ template <int DT, bool INDEXED>
 int launch_runs_dt(const void* x, const int32_t* perm, const int32_t* sids,
                    float* sums, int32_t* counts, const UpdateBufs& w,
                    int64_t B, int64_t N, int64_t K, int64_t D, bool overwrite,
-                   FinArgs<typename Elem<DT>::T> fin, const int32_t* ctrl,
-                   hipStream_t s) {
-#define FKC_RUNS(V, NI_)                                                      \
-  return launch_runs_t<DT, V, NI_, INDEXED>(x, perm, sids, sums, counts, w,  \
-                                            B, N, K, D, overwrite, fin, ctrl, \
-                                            s)
+                   const BlockArgs& blk, FinArgs<typename Elem<DT>::T> fin,
+                   const int32_t* ctrl, hipStream_t s) {
+#define FKC_RUNS(V, NI_)                                                     \
+  return launch_runs_t<DT, V, NI_, INDEXED>(x, perm, sids, sums, counts, w, \
+                                            B, N, K, D, overwrite, blk, fin, \
+                                            ctrl, s)
   const int vec = runs_vec(D), ni = runs_ni(D);
   if (vec == 2) {
     if (ni == 1) FKC_RUNS(2, 1);
@@ -771,44 +874,53 @@ template <int DT>
 int launch_update_t(const void* x, const int32_t* perm,
                     const int32_t* ids_sorted, float* sums, int32_t* counts,
                     const UpdateBufs& w, int64_t B, int64_t N, int64_t K,
-                    int64_t D, bool overwrite, FinArgs<typename Elem<DT>::T> fin,
-                    const int32_t* ctrl, hipStream_t s) {
+                    int64_t D, bool overwrite, int64_t seq,
+                    FinArgs<typename Elem<DT>::T> fin, const int32_t* ctrl,
+                    hipStream_t s) {
+  // With one block every run ends inside it and block partials are unused.
+  // The Lloyd loop (seq >= 0) sums full blocks inside update_runs, its flags
+  // tagged with the call's number; otherwise update_blocks does, tag 1.
+  const bool in_runs = seq >= 0 && w.nblocks > 1;
+  BlockArgs blk{w.bpart, w.bmeta, in_runs ? w.bctr : nullptr, (int)w.nblocks,
+                in_runs ? (int)(1 + seq % (INT_MAX - 1)) : 1};
   int rc = perm != nullptr
                ? launch_runs_dt<DT, true>(x, perm, ids_sorted, sums, counts, w,
-                                          B, N, K, D, overwrite, fin, ctrl, s)
+                                          B, N, K, D, overwrite, blk, fin,
+                                          ctrl, s)
                : launch_runs_dt<DT, false>(x, perm, ids_sorted, sums, counts,
-                                           w, B, N, K, D, overwrite, fin, ctrl,
-                                           s);
+                                           w, B, N, K, D, overwrite, blk, fin,
+                                           ctrl, s);
   if (rc) return rc;
-  // With one block every run ends inside it and block partials are unused.
-  if (w.nblocks > 1) {
+  if (w.nblocks > 1 && !in_runs) {
     dim3 bgrid((unsigned)((w.nblocks + 3) / 4), (unsigned)B);
     hipLaunchKernelGGL(update_blocks_kernel, bgrid, dim3(UT), 0, s, w.part,
                        w.meta, w.bpart, w.bmeta, (int)D, (int)w.nunits,
-                       (int)w.nblocks, ctrl);
+                       (int)w.nblocks, blk.tag, ctrl);
     rc = check_launch("update_blocks");
     if (rc) return rc;
   }
   dim3 grid((unsigned)((w.nunits + 3) / 4), (unsigned)B);
   hipLaunchKernelGGL((update_merge_kernel<DT>), grid, dim3(UT), 0, s, w.part,
                      w.meta, w.bpart, w.bmeta, sums, counts, (int)K, (int)D,
-                     (int)w.nunits, (int)w.nblocks, overwrite ? 1 : 0, fin,
-                     ctrl);
+                     (int)w.nunits, (int)w.nblocks, overwrite ? 1 : 0, blk.tag,
+                     blk.ctr, (int)w.nz, fin, ctrl);
   return check_launch("update_merge");
 }
 
 }  // namespace
 
 size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D) {
-  const int ur = choose_ur(B, N);
-  const int64_t nunits = (N + ur - 1) / ur;
-  const int64_t nblocks = (nunits + UB - 1) / UB;
-  Carve c(nullptr);
-  c.take<float>((size_t)B * nunits * 2 * D);     // unit head/tail partials
-  c.take<int32_t>((size_t)B * nunits * 4);       // unit metadata
-  c.take<float>((size_t)B * nblocks * D);        // block partials
-  c.take<int32_t>((size_t)B * nblocks * 2);      // block flag, row count
-  return c.used;
+  return carve_update(nullptr, B, N, D).used;
+}
+
+void update_control_region(void* ws, int64_t B, int64_t N, int64_t D,
+                           int32_t** p, int64_t* n) {
+  *p = nullptr;
+  *n = 0;
+  if (B == 0 || N == 0) return;
+  const UpdateBufs w = carve_update(ws, B, N, D);
+  *p = w.bmeta;
+  *n = w.nctl;
 }
 
 int launch_update(const void* x, const int32_t* perm,
@@ -816,7 +928,7 @@ int launch_update(const void* x, const int32_t* perm,
                   int64_t B, int64_t N, int64_t K, int64_t D, int dtype,
                   bool overwrite, void* ws, size_t ws_bytes,
                   const int32_t* ctrl, hipStream_t s, const UpdateFinalize* fin,
-                  bool* fused) {
+                  bool* fused, int64_t seq) {
   if (fused) *fused = false;
   if (B == 0) return FKC_OK;
   if (N == 0) {
@@ -832,15 +944,9 @@ int launch_update(const void* x, const int32_t* perm,
     return fail(FKC_ERR_WORKSPACE,
                 "centroid_update: workspace not %d-byte aligned",
                 kWorkspaceAlign);
-  const int ur = choose_ur(B, N);
-  UpdateBufs w;
-  w.nunits = (N + ur - 1) / ur;
-  w.nblocks = (w.nunits + UB - 1) / UB;
-  Carve c(ws);
-  w.part = c.take<float>((size_t)B * w.nunits * 2 * D);
-  w.meta = c.take<int32_t>((size_t)B * w.nunits * 4);
-  w.bpart = c.take<float>((size_t)B * w.nblocks * D);
-  w.bmeta = c.take<int32_t>((size_t)B * w.nblocks * 2);
+  if (seq >= 0 && !overwrite)
+    return fail(FKC_ERR_INVALID, "centroid_update: a sequenced call overwrites");
+  const UpdateBufs w = carve_update(ws, B, N, D);
   // Finalize fuses when a whole row fits one wave's column slices and LDS
   // row buffer (D <= 512; then grid.z == 1) and every label is valid.
   const bool fuse = fin != nullptr && fin->cent != nullptr && overwrite &&
@@ -852,21 +958,21 @@ int launch_update(const void* x, const int32_t* perm,
       FinArgs<float> f{fuse ? static_cast<float*>(fin->cent) : nullptr,
                        fuse ? fin->c_sq : nullptr, fuse ? fin->shift : nullptr};
       return launch_update_t<FKC_F32>(x, perm, ids_sorted, sums, counts, w, B,
-                                      N, K, D, overwrite, f, ctrl, s);
+                                      N, K, D, overwrite, seq, f, ctrl, s);
     }
     case FKC_F16: {
       using T = typename Elem<FKC_F16>::T;
       FinArgs<T> f{fuse ? static_cast<T*>(fin->cent) : nullptr,
                    fuse ? fin->c_sq : nullptr, fuse ? fin->shift : nullptr};
       return launch_update_t<FKC_F16>(x, perm, ids_sorted, sums, counts, w, B,
-                                      N, K, D, overwrite, f, ctrl, s);
+                                      N, K, D, overwrite, seq, f, ctrl, s);
     }
     case FKC_BF16: {
       using T = typename Elem<FKC_BF16>::T;
       FinArgs<T> f{fuse ? static_cast<T*>(fin->cent) : nullptr,
                    fuse ? fin->c_sq : nullptr, fuse ? fin->shift : nullptr};
       return launch_update_t<FKC_BF16>(x, perm, ids_sorted, sums, counts, w, B,
-                                       N, K, D, overwrite, f, ctrl, s);
+                                       N, K, D, overwrite, seq, f, ctrl, s);
     }
     default:
       return fail(FKC_ERR_INVALID, "centroid_update: unknown dtype %d", dtype);
