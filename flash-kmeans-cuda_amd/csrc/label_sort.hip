@@ -213,6 +213,16 @@ struct SweepArgs {
   int fuse;                // first pass that also counts every pass's digits
 };
 
+// Sum of v over the q lanes of the calling lane's group (q in {1, 2, 4, 8};
+// groups are aligned runs of q lanes), returned to every lane of the group:
+// DPP adds over quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror.
+__device__ inline int group_sum(int v, int q) {
+  if (q >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  if (q >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  if (q >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  return v;
+}
+
 // Published for this call: flag set and this call's epoch.
 __device__ inline bool st_published(uint64_t v, uint64_t tag) {
   const uint64_t hi = v & ~ST_CNT;
@@ -230,6 +240,8 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   __shared__ int gbase[256];
   __shared__ int dstart[256];
   __shared__ int wtot[8];
+  __shared__ int s_tot[256];   // the tile's count per digit
+  __shared__ int s_excl[256];  // exclusive prefix over earlier tiles; -1: stopped
   __shared__ int s_tile;
   __shared__ int s_recount;  // a digit of this tile stopped waiting
   __shared__ int s_short;    // the row barrier's wait ran out (fused)
@@ -331,6 +343,7 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
                          (tile == 0 ? ST_INC : ST_AGG) | a.tag | (uint64_t)total,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (fuse && total) atomicAdd(grow + tid, total);
+      s_tot[tid] = total;
     }
     if (fuse) {
       for (int p = 1; p < a.pd.passes; ++p) {
@@ -354,57 +367,149 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   if (fuse && tid == 0)
     __hip_atomic_fetch_add(crow + CTR_ARRIVE, 1ull, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-  bool stopped = false;  // this digit's walk ran out of spins
-  if (tid < nb) {
-    int64_t excl = 0;
-    if (tile > 0) {
-      // The walk reads LB predecessors' status words at once (one round
-      // trip per window instead of one per tile), then takes them newest
-      // first: counts add up until an inclusive prefix; a word not yet
-      // published ends the window, and the walk polls again from it.
-      const uint64_t* col = srow + tid;
-      int spins = 0;  // one budget for the whole walk
-      int t = tile - 1;
-      for (;;) {
-        if (spins >= a.spin_limit) {
-          stopped = true;
-          break;
-        }
-        uint64_t v[LB];
-#pragma unroll
-        for (int i = 0; i < LB; ++i)
-          v[i] = t - i >= 0 ? __hip_atomic_load(col + (size_t)(t - i) * 256,
-                                                __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT)
-                            : 0ull;
-        int used = 0;       // words of the window consumed
-        bool done = false;  // an inclusive prefix (or tile 0) was reached
-#pragma unroll
-        for (int i = 0; i < LB; ++i) {
-          if (!st_published(v[i], a.tag)) break;
-          excl += (int64_t)(v[i] & ST_CNT);
-          used = i + 1;
-          if ((v[i] & ST_INC) || t - i == 0) {
-            done = true;
+  // Look-back over earlier tiles' status words, per digit.  With one lane
+  // per digit the lane reads LB predecessors at once (one round trip per
+  // window), then takes them newest first: counts add up until an
+  // inclusive prefix (or tile 0); a word not yet published ends the window,
+  // and the walk polls again from it.  With more threads than digits, q
+  // lanes per digit (at most 8) walk together: lane j of a digit's group
+  // reads tiles t - j*LB .. t - j*LB - LB + 1, so one round trip covers
+  // q*LB predecessors, and every lane of the group derives the same walk
+  // state from a ballot and DPP sums.
+  int q = 1;
+  while (q < 8 && nb * q * 2 <= ST) q <<= 1;
+  bool stopped = false;  // this digit's walk ran out of spins (tid < nb)
+  if (q == 1) {
+    if (tid < nb) {
+      int64_t excl = 0;
+      if (tile > 0) {
+        const uint64_t* col = srow + tid;
+        int spins = 0;  // one budget for the whole walk
+        int t = tile - 1;
+        for (;;) {
+          if (spins >= a.spin_limit) {
+            stopped = true;
             break;
           }
+          uint64_t v[LB];
+#pragma unroll
+          for (int i = 0; i < LB; ++i)
+            v[i] = t - i >= 0 ? __hip_atomic_load(col + (size_t)(t - i) * 256,
+                                                  __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : 0ull;
+          int used = 0;       // words of the window consumed
+          bool done = false;  // an inclusive prefix (or tile 0) was reached
+#pragma unroll
+          for (int i = 0; i < LB; ++i) {
+            if (!st_published(v[i], a.tag)) break;
+            excl += (int64_t)(v[i] & ST_CNT);
+            used = i + 1;
+            if ((v[i] & ST_INC) || t - i == 0) {
+              done = true;
+              break;
+            }
+          }
+          if (done) break;
+          t -= used;
+          if (used < LB) {  // the next word is not published yet
+            ++spins;
+            __builtin_amdgcn_s_sleep(1);
+          }
         }
-        if (done) break;
-        t -= used;
-        if (used < LB) {  // the next word is not published yet
-          ++spins;
-          __builtin_amdgcn_s_sleep(1);
+        if (stopped)
+          s_recount = 1;
+        else
+          __hip_atomic_store(srow + (size_t)tile * 256 + tid,
+                             ST_INC | a.tag | (uint64_t)(excl + total),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      dstart[tid] = pre.x;
+      gbase[tid] = pre.y + (int)excl - pre.x;  // fused: pre.y == 0 here
+    }
+  } else {
+    const int ld = tid / q, lj = tid % q;  // digit, lane in its group
+    const int g0 = lane - lj;              // the group's first lane (q | 64)
+    bool gstop = false;                    // the group's walk ran out of spins
+    int64_t gexcl = 0;
+    const uint64_t* col = srow + (ld < nb ? ld : 0);
+    int spins = 0;  // one budget for the whole walk
+    int t = tile - 1;
+    bool gdone = !(ld < nb && tile > 0);
+    while (__builtin_amdgcn_ballot_w64(!gdone) != 0) {  // wave-uniform
+      if (!gdone && spins >= a.spin_limit) {
+        gstop = true;
+        gdone = true;
+      }
+      const int tb = t - lj * LB;  // newest tile of this lane's share
+      uint64_t v[LB];
+#pragma unroll
+      for (int i = 0; i < LB; ++i)
+        v[i] = !gdone && tb - i >= 0
+                   ? __hip_atomic_load(col + (size_t)(tb - i) * 256,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : 0ull;
+      uint32_t sum = 0;  // counts of this lane's consumed words (< 2^32)
+      int used = 0;      // words of the share consumed
+      bool inc = false;  // an inclusive prefix (or tile 0) was reached
+      bool go = true;
+#pragma unroll
+      for (int i = 0; i < LB; ++i) {
+        if (go) {
+          if (!st_published(v[i], a.tag)) {
+            go = false;
+          } else {
+            sum += (uint32_t)(v[i] & ST_CNT);
+            used = i + 1;
+            if ((v[i] & ST_INC) || tb - i == 0) {
+              inc = true;
+              go = false;
+            }
+          }
         }
       }
-      if (stopped)
-        s_recount = 1;
-      else
-        __hip_atomic_store(srow + (size_t)tile * 256 + tid,
-                           ST_INC | a.tag | (uint64_t)(excl + total),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // The group's first lane js whose share did not pass through whole:
+      // lanes 0 .. js consumed their words this step (lanes before js all
+      // LB of them), so the step's counts, words consumed and inclusive
+      // flag are group sums over those lanes.
+      const bool full = !gdone && used == LB && !inc;
+      const uint64_t nf = __builtin_amdgcn_ballot_w64(!full);
+      const uint32_t mg = (uint32_t)(nf >> g0) & ((1u << q) - 1u);
+      const int js = mg ? __builtin_ctz(mg) : q;
+      const bool mine = lj <= js;
+      const uint32_t tot = (uint32_t)group_sum(mine ? (int)sum : 0, q);
+      const int pk = group_sum(mine ? used | (inc ? 256 : 0) : 0, q);
+      if (!gdone) {
+        gexcl += tot;
+        if (pk >> 8) {
+          gdone = true;
+        } else {
+          t -= pk & 255;
+          if (js < q) {  // a word not yet published
+            ++spins;
+            __builtin_amdgcn_s_sleep(1);
+          }
+        }
+      }
     }
-    dstart[tid] = pre.x;
-    gbase[tid] = pre.y + (int)excl - pre.x;  // fused: pre.y == 0 here
+    if (lj == 0 && ld < nb) {
+      if (tile > 0) {
+        if (gstop)
+          s_recount = 1;
+        else
+          __hip_atomic_store(srow + (size_t)tile * 256 + ld,
+                             ST_INC | a.tag | (uint64_t)(gexcl + s_tot[ld]),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      s_excl[ld] = gstop ? -1 : (int)gexcl;
+    }
+    __syncthreads();
+    if (tid < nb) {
+      const int e = s_excl[tid];
+      stopped = e < 0;
+      dstart[tid] = pre.x;
+      gbase[tid] = pre.y + (stopped ? 0 : e) - pre.x;  // fused: pre.y == 0
+    }
   }
   __syncthreads();
   if (s_recount) {  // workgroup-uniform; never taken in a normal run
