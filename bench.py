@@ -14,9 +14,9 @@ Reported:
   value / ms_per_step   end-to-end ms per Lloyd iteration (lower is better)
   assign_tflops         2*B*N*K*D / mean assign kernel time, the kernel time
                         measured with HIP events stamped by the dispatch of
-                        the assign launch of every 5th iteration of the timed
-                        region (iterations 0, 5, 10, ...), on the launch
-                        stream
+                        the assign launch of the middle iteration of every
+                        run of 5 in the timed region (iterations 2, 7, 12,
+                        ...), on the launch stream
   roofline              assign kernel against the fp16 dense MFMA peak
   cpu_baseline          the CPU oracle (numpy fp32 BLAS restatement of the
                         same loop) on a bounded sample, scaled to full N
@@ -50,7 +50,7 @@ sys.path.insert(0, HERE)
 PEAK_TFLOPS_F16 = 2500.0          # MI355X dense fp16/bf16 MFMA
 PEAK_TFLOPS_F32 = 157.3           # MI355X fp32 (the fp32 route runs on the VALU)
 METRIC_C5 = "assign TFLOPS + end-to-end ms/iter at (1,524K,8192,128) fp16, 1 MI355X"
-PROFILE_PERIOD = 5                # event-time the assign of every 5th timed iteration
+PROFILE_PERIOD = 5                # event-time the assign of one timed iteration in 5
 PEAK_HBM_GBS = 8000.0
 REF_MS_PER_ITER = {"c5": 6.179, "c3": 0.489, "c2": 0.129}   # README.md:31-34 (RTX 4090)
 REF_ASSIGN_TFLOPS = {"c5": 185.0, "c3": 171.0, "c2": 92.0}  # README.md:21-24
@@ -391,10 +391,13 @@ def main() -> int:
         batch_kmeans_Euclid(x, cfg.K, max_iters=args.warmup, tol=0.0, init_centroids=init)
     torch.cuda.synchronize()
 
-    # timed: exactly --steps Lloyd iterations; the assign launch of every
-    # PROFILE_PERIOD-th iteration is event-timed (each timed launch costs the
-    # stream ~9 us of event handling, kept out of the other iterations)
-    _lib.lib.fkc_profile_enable(PROFILE_PERIOD)
+    # timed: exactly --steps Lloyd iterations; the assign launch of the
+    # middle iteration of every run of PROFILE_PERIOD is event-timed (each
+    # timed launch costs the stream ~9 us of event handling, kept out of the
+    # other iterations; midpoints, because the clock still drifts over the
+    # first timed iterations after a short warm-up)
+    period = PROFILE_PERIOD if args.steps > PROFILE_PERIOD // 2 else 1
+    _lib.lib.fkc_profile_enable(period)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ids, cents, n = batch_kmeans_Euclid(x, cfg.K, max_iters=args.steps, tol=0.0,
@@ -407,7 +410,7 @@ def main() -> int:
                "profile")
     _lib.lib.fkc_profile_enable(0)
     assert n == args.steps
-    assert launches.value == (args.steps + PROFILE_PERIOD - 1) // PROFILE_PERIOD
+    assert launches.value == (args.steps - period // 2 + period - 1) // period
 
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     assign_ms = tot.value / launches.value

@@ -449,7 +449,11 @@ int lloyd_run(const void* x, const void* init, void* centroids,
     hipEvent_t e0 = nullptr, e1 = nullptr;
     const int period =
         profile ? g_prof.period.load(std::memory_order_relaxed) : 0;
-    if (period > 0 && it % period == 0) {
+    // The middle iteration of each run of `period` (k/2, k/2 + k, ...):
+    // with a clock that still drifts over the first iterations, midpoints
+    // estimate the mean launch time without the bias of always sampling a
+    // run's first iteration.
+    if (period > 0 && it % period == period / 2) {
       if (hipEventCreateWithFlags(&e0, hipEventDisableSystemFence) != hipSuccess)
         return fail(FKC_ERR_LAUNCH, "kmeans_lloyd: profiling event creation failed");
       if (hipEventCreateWithFlags(&e1, hipEventDisableSystemFence) != hipSuccess) {

@@ -270,9 +270,10 @@ FKC_CAPI int fkc_kmeans_lloyd_noalloc(const void* x, const void* init_centroids,
 
 /*
  * Profiling hook for benchmarks (no counterpart in the reference): with
- * enable = k > 0, fkc_kmeans_lloyd times the assignment launch of every k-th
- * loop iteration (iterations 0, k, 2k, ...) with HIP events stamped by the
- * launch's dispatch on its stream (each timed launch costs the stream a few
+ * enable = k > 0, fkc_kmeans_lloyd times the assignment launch of the middle
+ * iteration of every run of k loop iterations (iterations k/2, k/2 + k,
+ * k/2 + 2k, ..., integer division) with HIP events stamped by the launch's
+ * dispatch on its stream (each timed launch costs the stream a few
  * microseconds, so k > 1 keeps that out of most iterations); enable = 0
  * turns it off.  fkc_profile_assign_ms() synchronises on the recorded events
  * and returns the summed assignment time in ms and the timed launch count.

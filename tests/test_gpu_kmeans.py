@@ -520,3 +520,26 @@ def test_two_threads_on_two_streams_with_profiling():
     assert launches.value == iters * len(jobs) and tot.value > 0.0
     for a, b in zip(alone, out):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and a[2] == b[2]
+
+
+@pytest.mark.parametrize("period,iters,want", [(5, 12, 2), (5, 2, 0), (5, 3, 1), (4, 9, 2), (1, 3, 3)])
+def test_profile_hook_times_stratum_midpoints(period, iters, want):
+    """fkc_profile_enable(k) times the middle iteration of every run of k
+    (iterations k/2, k/2 + k, ...): the launch count follows, and a loop
+    shorter than k/2 + 1 iterations times none."""
+    from flash_kmeans_cuda import _lib, batch_kmeans_Euclid, synth
+    L = _lib.lib
+    cfg = synth.CONFIGS["c2"]
+    x, init = synth.make(cfg, N=4096)
+    xt, it = _T(x, "f16"), _T(init, "f16")
+    tot = _lib.ctypes.c_double(0.0)
+    launches = _lib.ctypes.c_int64(0)
+    L.fkc_profile_enable(period)
+    try:
+        batch_kmeans_Euclid(xt, cfg.K, max_iters=iters, init_centroids=it)
+        _lib.check(L.fkc_profile_assign_ms(_lib.ctypes.byref(tot),
+                                           _lib.ctypes.byref(launches)), "profile")
+    finally:
+        L.fkc_profile_enable(0)
+    assert launches.value == want
+    assert (tot.value > 0.0) == (want > 0)
