@@ -62,7 +62,8 @@ int sort_tile_override() {
   const char* s = std::getenv("FKC_SORT_TILE");
   if (!s) return 0;
   const int v = std::atoi(s);
-  return (v == 256 || v == 512 || v == 1024 || v == 2048 || v == 4096) ? v : 0;
+  return (v == 256 || v == 512 || v == 1024 || v == 2048 || v == 4096 ||
+          v == 8192) ? v : 0;
 }
 
 int save_override() {

@@ -82,7 +82,7 @@ int label_sort_reset(void* ws, int64_t B, int64_t N, int64_t K, hipStream_t s);
 // launch): *p, *n (n = 0 when B * N == 0).
 void label_sort_reset_region(void* ws, int64_t B, int64_t N, int64_t K,
                              int32_t** p, int64_t* n);
-// FKC_SORT_TILE=256|512|1024|2048|4096: keys per sort tile; 0 = auto.
+// FKC_SORT_TILE=256|512|1024|2048|4096|8192: keys per sort tile; 0 = auto.
 int sort_tile_override();
 // FKC_SORT_SPIN=n (n >= 0, tests): spin budget of the sort's waits instead
 // of dflt; 0 sends every wait (look-back walk, row barrier) to its recount.

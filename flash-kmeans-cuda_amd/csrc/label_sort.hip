@@ -89,7 +89,7 @@ struct PassDesc {
 template <int TILE_>
 struct Geom {
   static constexpr int TILE = TILE_;
-  static constexpr int ST = TILE_ >= 4096 ? 512 : 256;
+  static constexpr int ST = TILE_ >= 8192 ? 1024 : (TILE_ >= 4096 ? 512 : 256);
   static constexpr int SW = ST / 64;
   static constexpr int PER_WAVE = TILE / SW;
   static constexpr int CHUNKS = PER_WAVE / 64;
@@ -618,11 +618,14 @@ SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
   // tile plus about 20 ns of look-back chain per tile, so fewer, larger
   // tiles win even when they leave CUs idle (measured at N = 524288,
   // K = 8192: 52 / 32 / 21 / 16 / 13.5 us per pass for 256 .. 4096-key
-  // tiles; 8192-key tiles, 16 keys per thread, took 16.4 us).  With at most 65536 keys in all the chain is short and smaller
-  // tiles shorten each tile's own work (1024 / 2048 / 4096-key tiles, us per
-  // pass: 8.6 / 10.4 / 10.7 at B x N = 32768; 8.6 / 9.5 / 9.4 at 65536; but
-  // 10.2 / 10.2 / 9.8 at 131072 and 12.0 / 10.4 / 9.6 at 8 x 65536).
-  // FKC_SORT_TILE overrides.
+  // tiles).  8192-key tiles lose: with 16 keys per thread a pass took
+  // 16.4 us, and on 1024 threads (8 keys each) the 89 KB workgroup runs
+  // alone on its CU (the whole c5 sort 37.3 vs 35.1 us).  With at most
+  // 65536 keys in all the chain is short and smaller tiles shorten each
+  // tile's own work (1024 / 2048 / 4096-key tiles, us per pass: 8.6 / 10.4
+  // / 10.7 at B x N = 32768; 8.6 / 9.5 / 9.4 at 65536; but 10.2 / 10.2 /
+  // 9.8 at 131072 and 12.0 / 10.4 / 9.6 at 8 x 65536).  FKC_SORT_TILE
+  // overrides.
   int tile = B * N <= 65536 ? 1024 : 4096;
   if (const int o = sort_tile_override()) tile = o;
   p.tile = tile;
@@ -714,6 +717,7 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
       case 512: launch_onesweep<512>(grid, s, a); break;
       case 1024: launch_onesweep<1024>(grid, s, a); break;
       case 2048: launch_onesweep<2048>(grid, s, a); break;
+      case 8192: launch_onesweep<8192>(grid, s, a); break;
       default: launch_onesweep<4096>(grid, s, a); break;
     }
     rc = check_launch("sort_onesweep");

@@ -81,7 +81,7 @@ def test_label_sort_zipf_skew():
     assert np.array_equal(_np(p), ep) and np.array_equal(_np(s), es)
 
 
-@pytest.mark.parametrize("tile", [256, 512, 1024, 2048, 4096])
+@pytest.mark.parametrize("tile", [256, 512, 1024, 2048, 4096, 8192])
 @pytest.mark.parametrize("B,N,K,pattern", [
     (2, 100000, 8192, "random"), (1, 70001, 70000, "random"),
     (1, 300000, 4096, "same"), (3, 9000, 9000, "descending"),
@@ -247,7 +247,8 @@ def test_finalize_in_place():
 @pytest.mark.parametrize("fuse", [True, False])
 @pytest.mark.parametrize("B,N,K,tile", [(1, 100000, 8192, 4096), (2, 70001, 70000, 1024),
                                         (1, 524288, 8192, 4096), (3, 9000, 300, 256),
-                                        (2, 300000, 1000, 1024)])
+                                        (2, 300000, 1000, 1024), (1, 524288, 8192, 8192),
+                                        (3, 300000, 2000, 8192)])
 def test_label_sort_recount_path(monkeypatch, B, N, K, tile, fuse):
     """With a zero spin budget (FKC_SORT_SPIN=0) every wait gives up at
     once: each tile after the first recounts its prefix from the pass's
