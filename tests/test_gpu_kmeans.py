@@ -231,6 +231,27 @@ def test_loop_sort_paths_agree(monkeypatch, cfg_name, N):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), (fuse, spin)
 
 
+@pytest.mark.parametrize("tile", [256, 512])
+def test_loop_with_counter_ordered_sort_tiles(monkeypatch, tile):
+    """Sort grids of more than 256 tiles take their tile index from a per-row
+    counter that grows over the loop's iterations (each call offsets it by
+    its sequence number) and count digits in a separate kernel.  c4's 8
+    batch rows at N = 16384 make 512 tiles of 256 keys (that path) or 256
+    tiles of 512 keys (resident: block-index tiles, digits counted in the
+    first pass); either way the loop gives the same bits as with the
+    default tiles, twice in a row on fresh workspaces."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    cfg = synth.CONFIGS["c4"]
+    x, init = synth.make(cfg, N=16384)
+    xt, it = _T(x, cfg.dtype), _T(init, cfg.dtype)
+    a = batch_kmeans_Euclid(xt, cfg.K, max_iters=6, init_centroids=it)
+    monkeypatch.setenv("FKC_SORT_TILE", str(tile))
+    b = batch_kmeans_Euclid(xt, cfg.K, max_iters=6, init_centroids=it)
+    c = batch_kmeans_Euclid(xt, cfg.K, max_iters=6, init_centroids=it)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    assert torch.equal(b[0], c[0]) and torch.equal(b[1], c[1])
+
+
 def test_verbose_path_equals_fused_loop(capsys):
     from flash_kmeans_cuda import batch_kmeans_Euclid, synth
     cfg = synth.CONFIGS["c2"]
