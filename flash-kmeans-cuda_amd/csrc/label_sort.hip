@@ -624,9 +624,12 @@ SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
   // 65536 keys in all the chain is short and smaller tiles shorten each
   // tile's own work (1024 / 2048 / 4096-key tiles, us per pass: 8.6 / 10.4
   // / 10.7 at B x N = 32768; 8.6 / 9.5 / 9.4 at 65536; but 10.2 / 10.2 /
-  // 9.8 at 131072 and 12.0 / 10.4 / 9.6 at 8 x 65536).  FKC_SORT_TILE
+  // 9.8 at 131072 and 12.0 / 10.4 / 9.6 at 8 x 65536), and up to 32768
+  // keys 512-key tiles shorten it once more (Lloyd loop, us per iteration
+  // with 512 / 1024-key tiles: 30.8-31.1 / 31.9-32.6 at 4096 keys, 30.0-30.2
+  // / 30.3-30.7 at 32768; at 65536 they lose 2.5 us).  FKC_SORT_TILE
   // overrides.
-  int tile = B * N <= 65536 ? 1024 : 4096;
+  int tile = B * N <= 32768 ? 512 : (B * N <= 65536 ? 1024 : 4096);
   if (const int o = sort_tile_override()) tile = o;
   p.tile = tile;
   p.ntiles = (N + p.tile - 1) / p.tile;
