@@ -47,7 +47,7 @@ def _sort_ws(B, N, K):
     return ws
 
 
-def _health(ws):
+def _recounts(ws):
     """Word 0 of the workspace (recounts); word 1 (tiles whose counter was
     out of step with the call sequence) must stay 0."""
     torch.cuda.synchronize()
@@ -68,7 +68,7 @@ def test_label_sort_bit_exact(B, N, K):
     es, ep = O.label_sort(ids, K)
     assert np.array_equal(_np(p), ep)
     assert np.array_equal(_np(s), es)
-    assert _health(ws) == 0
+    assert _recounts(ws) == 0
 
 
 def test_label_sort_zipf_skew():
@@ -92,7 +92,7 @@ def test_label_sort_every_tile_size(monkeypatch, tile, B, N, K, pattern):
     on its predecessors for every digit), bit-exact against the stable sort;
     each case is sorted twice in a row on one workspace that starts out
     filled with stale bytes (the second call finds the first call's counters
-    and status words), and the sort's health word stays 0."""
+    and status words), and no wait ran out (the recount word stays 0)."""
     from flash_kmeans_cuda.ops import label_sort
     monkeypatch.setenv("FKC_SORT_TILE", str(tile))
     rng = np.random.default_rng(tile + N)
@@ -108,7 +108,7 @@ def test_label_sort_every_tile_size(monkeypatch, tile, B, N, K, pattern):
         s, p = label_sort(_t(ids), K, workspace=ws)
         assert np.array_equal(_np(p), ep)
         assert np.array_equal(_np(s), es)
-        assert _health(ws) == 0
+        assert _recounts(ws) == 0
 
 
 def _update_case(B, N, K, D, dtype, seed, invalid=False, zipf=False):
@@ -272,10 +272,10 @@ def test_label_sort_recount_path(monkeypatch, B, N, K, tile, fuse):
     bits = int(np.ceil(np.log2(K + 1)))
     passes = (bits + 7) // 8
     fused = fuse and B * ntiles <= 256
-    assert _health(ws) == B * passes * (ntiles - 1) + (B * ntiles if fused else 0)
+    assert _recounts(ws) == B * passes * (ntiles - 1) + (B * ntiles if fused else 0)
     monkeypatch.delenv("FKC_SORT_SPIN")
     s2, p2 = label_sort(_t(ids), K, workspace=ws)
-    assert torch.equal(s2, s) and torch.equal(p2, p) and _health(ws) == 0
+    assert torch.equal(s2, s) and torch.equal(p2, p) and _recounts(ws) == 0
 
 
 def _add_mode(x, perm, ids, K, dtype, indexed=True):
