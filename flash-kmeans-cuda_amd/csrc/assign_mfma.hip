@@ -670,21 +670,18 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
         ar[r][s] = (!padded || seg < dsegs) ? v : u32x4{0u, 0u, 0u, 0u};
       }
     }
-    // Accumulator rows 4g+j of this lane belong to point 4g+j of the tile;
-    // lane 4g+j (g = 0 there) holds that point's base and candidate c_sq.
-    int rbase[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) rbase[j] = __shfl(base, 4 * g + j, 64);
+    // Only the diagonal of each chain is read: accumulator row i = col
+    // (element e = col & 3 of the lane with g == col / 4) is point col
+    // against its own candidate, and that lane loaded this very point's
+    // base and candidate c_sq.  So every lane seeds all four rows with its
+    // own point's value: the diagonal gets the loop's seed, the rest is
+    // never read (no cross-lane exchange of bases or c_sq is needed).
     const int e = col & 3;  // this lane's diagonal element when g == col/4
     float dv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      f32x4 acc;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float q = __shfl(cq[r], 4 * g + j, 64);
-        acc[j] = rbase[j] + r < K ? -0.5f * q : -INFINITY;
-      }
+      const float seed = base + r < K ? -0.5f * cq[r] : -INFINITY;
+      f32x4 acc = {seed, seed, seed, seed};
 #pragma unroll
       for (int s = 0; s < DS2; ++s) acc = mfma16<DT>(ar[r][s], xr[p][s], acc);
       float d = acc[0];
