@@ -286,6 +286,25 @@ def test_few_clusters_many_points(B, N, K, D, dtype):
     assert np.linalg.norm(gc - oc) / np.linalg.norm(oc) < 1e-2
 
 
+@pytest.mark.parametrize("B,N,K,D,dtype", [(1, 200000, 2, 1100, "f16"), (2, 120000, 3, 600, "bf16")])
+def test_few_clusters_wide_rows(B, N, K, D, dtype):
+    """Runs over many full 64-unit blocks at widths whose update splits the
+    row over several column blocks (grid z > 1): the loop sums each block
+    inside its run kernel, one arrival counter per column block, and must
+    equal the per-op path (separate block kernel) bit for bit."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    rng = np.random.default_rng(N + D)
+    centres = 3 * rng.standard_normal((K, D)).astype(np.float32)
+    blob = rng.integers(0, K, (B, N))
+    x = O.from_f32(centres[blob] + rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    init = np.ascontiguousarray(x[:, :K])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    del x
+    a = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it, verbose=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 @pytest.mark.parametrize("D,dtype", [(512, "bf16"), (520, "f32"), (264, "f16"), (3, "f32")])
 def test_fused_loop_equals_per_op_path_across_widths(D, dtype):
     """The loop finalizes inside the update for D <= 512 and with its own
