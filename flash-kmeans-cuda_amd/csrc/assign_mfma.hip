@@ -182,6 +182,7 @@ __device__ inline void fold_saved(const f32x4& acc, float& best, int& bblk,
 template <int DT, int DS2, int PT, bool PAD, bool EXACT, bool SAVE>
 __global__ void __launch_bounds__(THREADS,
                                   PT == 8 ? 2
+                                  : (SAVE && DS2 == 2) ? 3
                                   : (DS2 == 2 && PT <= 4) ? 4
                                   : (PT * DS2 <= 16 && DS2 <= 9) ? FKC_AB
                                                                  : 1)
@@ -797,8 +798,8 @@ constexpr MfmaLauncher entry(bool pad, bool exact, bool save) {
     return nullptr;
   } else if constexpr (PT * DS2 * 4 <= 64) {
     if (save) {
-      // Saved-score fold: four tiles at D = 97..128, unpadded only.
-      if constexpr (PT == 4 && DS2 == 4) {
+      // Saved-score fold: four tiles at D = 64 or 97..128, unpadded only.
+      if constexpr (PT == 4 && (DS2 == 4 || DS2 == 2)) {
         if (!pad && !exact) return &launch_mfma_t<DT, DS2, PT, false, false, true>;
       }
       return nullptr;
@@ -897,15 +898,23 @@ struct Plan {
   bool pad, exact, save;
 };
 
-// The saved-score fold (four tiles at D = 97..128, unpadded) runs at two
-// waves per SIMD; it is taken where the launch has at most two workgroups
-// per CU anyway (grids of <= 512 workgroups), so the spare registers cost
-// no occupancy.  FKC_SAVE=0/1 forces it off / on where it exists.
+// The saved-score fold keeps the best block's four scores per lane, so the
+// winner needs no re-score: the re-score reads four full candidate rows per
+// point (512 B at D = 64, bf16), which at the end of a round of workgroups
+// is all CU-L1 traffic with the matrix cores idle.  Four tiles, unpadded:
+// at D = 97..128 it runs at two waves per SIMD and is taken where the
+// launch has at most two workgroups per CU anyway (grids of <= 512
+// workgroups); at D = 64 it costs a wave per SIMD (163 VGPRs, three waves)
+// and four selects per 16-centroid block, which pays for K (per slice) <=
+// 1024 (same-box assign times against the re-score, bf16: (4, 100000, 600)
+// -25%, (1, 262144, 1024) -9.6%, (8, 65536, 1024) -2.4% to -6.7%; but
+// (8, 65536, 2048) +8.3%, (1, 524288, 2048) +7.6%, K = 4096 / 8192
+// +14 / +15%).  FKC_SAVE=0/1 forces it off / on where it exists.
 static bool use_save(const Plan& p, int64_t wgs) {
-  if (p.pt != 4 || p.ds2 != 4 || p.pad || p.exact) return false;
+  if (p.pt != 4 || (p.ds2 != 4 && p.ds2 != 2) || p.pad || p.exact) return false;
   const int o = save_override();
   if (o >= 0) return o == 1;
-  return wgs <= 512;
+  return p.ds2 == 4 ? wgs <= 512 : p.kspan <= 1024;
 }
 
 // Launch plan.  K is sliced only when no unsliced grid fills the chip (few
