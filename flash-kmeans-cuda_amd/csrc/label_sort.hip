@@ -234,8 +234,8 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   constexpr int SW = Geom<TILE>::SW;
   constexpr int PER_WAVE = Geom<TILE>::PER_WAVE;
   constexpr int CHUNKS = Geom<TILE>::CHUNKS;
-  if (loop_done(a.ctrl)) return;
   __shared__ int cnt[SW][256];
+  __shared__ unsigned long long lmask[SW][256];  // ranking: lanes per digit
   __shared__ int hx[MAXP - 1][256];  // fused: digit counts of later passes
   __shared__ int gbase[256];
   __shared__ int dstart[256];
@@ -248,7 +248,11 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   __shared__ int32_t skey[TILE];
   __shared__ int32_t sval[TILE];
   const int N = a.N, K = a.K;
-  const int shift = a.pd.shift[a.pass], bits = a.pd.bits[a.pass];
+  // Pass parameters are grid-uniform: scalar registers (read from the
+  // argument block once, not per chunk).
+  const int npass = __builtin_amdgcn_readfirstlane(a.pd.passes);
+  const int shift = __builtin_amdgcn_readfirstlane(a.pd.shift[a.pass]);
+  const int bits = __builtin_amdgcn_readfirstlane(a.pd.bits[a.pass]);
   const bool fuse = a.fuse != 0;
   const int nb = 1 << bits;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -257,11 +261,36 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   int32_t* grow = a.gcnt + (size_t)b * MAXP * 256;
   uint64_t* crow = a.ctr + (size_t)b * CTR;
   uint64_t* srow = a.status + (size_t)b * a.slen;
+  const int32_t* kb = a.keys_in + (size_t)b * N;
+  const int32_t* vb = a.vals_in ? a.vals_in + (size_t)b * N : nullptr;
+  // Loads are unconditional (index clamped to the row, a first pass
+  // re-reading the keys where it has no payload) so that all of them are in
+  // flight at once: a load under a branch makes the compiler wait for it at
+  // the join.  Lanes past N are masked in the ranking; the identity payload
+  // is substituted at placement.
+  const int32_t* vsrc = vb ? vb : kb;
+  int32_t kk[CHUNKS], vv[CHUNKS];
+  auto load_tile = [&](int t) {
+    const int base = t * TILE + wave * PER_WAVE;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int n = min(base + c * 64 + lane, N - 1);
+      kk[c] = kb[n];
+      vv[c] = vsrc[n];
+    }
+  };
+  // A resident grid's tile is its block index: its keys are in flight
+  // before the control word is even read (a finished loop then drops them).
+  if (!a.dyn_tiles) load_tile((int)blockIdx.x);
+  if (loop_done(a.ctrl)) return;
   // The pass's global digit count does not depend on the tile: its load is
   // in flight together with the tile-counter atomic.  (A fused pass has it
   // only after the row barrier.)
   int gc = (!fuse && tid < nb) ? grow[a.pass * 256 + tid] : 0;
-  for (int i = tid; i < SW * 256; i += ST) (&cnt[0][0])[i] = 0;
+  for (int i = tid; i < SW * 256; i += ST) {
+    (&cnt[0][0])[i] = 0;
+    (&lmask[0][0])[i] = 0ull;
+  }
   if (fuse)
     for (int i = tid; i < (MAXP - 1) * 256; i += ST) (&hx[0][0])[i] = 0;
   // Tile index: with dyn_tiles, the order in which workgroups start (the
@@ -287,43 +316,65 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
     if (tid == 0) atomicAdd(a.err + 1, 1);
     return;
   }
+  if (a.dyn_tiles) load_tile(tile);
 
-  const int32_t* kb = a.keys_in + (size_t)b * N;
-  const int32_t* vb = a.vals_in ? a.vals_in + (size_t)b * N : nullptr;
   const int tbase = tile * TILE;
   const int tn = min(TILE, N - tbase);  // keys in this tile
   const int base = tbase + wave * PER_WAVE;
-  int32_t kk[CHUNKS], vv[CHUNKS];
   int rank[CHUNKS], dig[CHUNKS];
+  uint64_t match[CHUNKS];
+  int lead[CHUNKS];
   const uint32_t dmask = (uint32_t)(nb - 1);
+  // Later passes' digit fields (fused first pass).
+  uint32_t hsh[MAXP - 1], hmask[MAXP - 1];
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int n = base + c * 64 + lane;
-    const bool valid = n < N;
-    kk[c] = valid ? kb[n] : 0;
-    vv[c] = valid ? (vb ? vb[n] : n) : 0;
+  for (int p = 0; p < MAXP - 1; ++p) {
+    hsh[p] = (uint32_t)__builtin_amdgcn_readfirstlane(a.pd.shift[p + 1]);
+    hmask[p] =
+        (1u << __builtin_amdgcn_readfirstlane(a.pd.bits[p + 1])) - 1u;
   }
+  // Per 64-key chunk: the mask of lanes holding the lane's digit
+  // ("multi-split"): every lane ORs its lane bit into the wave's LDS word
+  // for its digit and reads the word back, and the word is cleared for the
+  // next chunk (an OR does not depend on the order of the lanes, and a
+  // wave's LDS operations execute in issue order, so the read sees exactly
+  // this chunk's bits; one LDS round trip instead of a ballot per digit
+  // bit, about 11 vector instructions each).  The digit's first lane then
+  // adds the group's size to the wave's count with an LDS atomic that
+  // returns the count before it; the atomics of all chunks issue back to
+  // back and each returns the count after the wave's earlier chunks.
+  const unsigned long long mybit = 1ull << lane;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const bool valid = base + c * 64 + lane < N;
     const uint32_t key = sort_key(kk[c], K);
     const uint32_t d = (key >> shift) & dmask;
-    uint64_t match = __builtin_amdgcn_ballot_w64(valid);
-    for (int bit = 0; bit < bits; ++bit) {
-      const bool on = (d >> bit) & 1u;
-      const uint64_t bal = __builtin_amdgcn_ballot_w64(on);
-      match &= on ? bal : ~bal;
-    }
-    const uint32_t below = lanes_below(match);
-    const int old = cnt[wave][d];
-    if (valid && below == 0) cnt[wave][d] = old + __popcll(match);
-    rank[c] = valid ? old + (int)below : -1;
+    unsigned long long* w = &lmask[wave][d];
+    __hip_atomic_fetch_or(w, valid ? mybit : 0ull, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_WORKGROUP);
+    const uint64_t m = __hip_atomic_load(w, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    match[c] = m;
     dig[c] = (int)d;
-    if (fuse && valid)
-      for (int p = 1; p < a.pd.passes; ++p)
-        atomicAdd(&hx[p - 1][(key >> a.pd.shift[p]) &
-                             ((1u << a.pd.bits[p]) - 1u)],
-                  1);
+    int o = 0;
+    if (valid && lanes_below(m) == 0) o = atomicAdd(&cnt[wave][d], __popcll(m));
+    lead[c] = o;
+    if (fuse && valid) {
+#pragma unroll
+      for (int p = 0; p < MAXP - 1; ++p)
+        if (p + 1 < npass) atomicAdd(&hx[p][(key >> hsh[p]) & hmask[p]], 1);
+    }
+  }
+  // The count before the chunk reaches the digit's other lanes from its
+  // first lane.
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const bool valid = base + c * 64 + lane < N;
+    const uint64_t m = match[c];
+    const int src = m ? (int)__builtin_ctzll(m) : lane;
+    const int old = __shfl(lead[c], src, 64);
+    rank[c] = valid ? old + (int)lanes_below(m) : -1;
   }
   __syncthreads();
 
@@ -334,10 +385,13 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   int total = 0;
   if (tid < 256) {
     if (tid < nb) {
+      int v[SW];
+#pragma unroll
+      for (int w = 0; w < SW; ++w) v[w] = cnt[w][tid];
+#pragma unroll
       for (int w = 0; w < SW; ++w) {
-        const int v = cnt[w][tid];
         cnt[w][tid] = total;
-        total += v;
+        total += v[w];
       }
       __hip_atomic_store(srow + (size_t)tile * 256 + tid,
                          (tile == 0 ? ST_INC : ST_AGG) | a.tag | (uint64_t)total,
@@ -577,18 +631,22 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
     if (rank[c] >= 0) {
       const int pos = dstart[dig[c]] + cnt[wave][dig[c]] + rank[c];
       skey[pos] = kk[c];
-      sval[pos] = vv[c];
+      sval[pos] = vb ? vv[c] : base + c * 64 + lane;
     }
   }
   __syncthreads();
   int32_t* ko = a.keys_out + (size_t)b * N;
   int32_t* vo = a.vals_out + (size_t)b * N;
-  for (int i = tid; i < tn; i += ST) {
-    const int32_t key = skey[i];
-    const int d = (int)((sort_key(key, K) >> shift) & dmask);
-    const int pos = gbase[d] + i;
-    ko[pos] = key;
-    vo[pos] = sval[i];
+#pragma unroll
+  for (int j = 0; j < TILE / ST; ++j) {
+    const int i = tid + j * ST;
+    if (i < tn) {
+      const int32_t key = skey[i];
+      const int d = (int)((sort_key(key, K) >> shift) & dmask);
+      const int pos = gbase[d] + i;
+      ko[pos] = key;
+      vo[pos] = sval[i];
+    }
   }
 }
 
