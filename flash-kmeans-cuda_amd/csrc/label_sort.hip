@@ -164,26 +164,36 @@ sort_upsweep_kernel(const int32_t* __restrict__ keys, int N, int K,
   }
 }
 
+// Inclusive scan over the 64 lanes by DPP adds: row_shr 1, 2, 4, 8 scan
+// each 16-lane row, row_bcast:15 adds row 0's total to row 1 and row 2's to
+// row 3, row_bcast:31 adds lane 31 (rows 0 and 1) to rows 2 and 3.  Lanes
+// without a source add the `old` operand, 0.  (A __shfl_up ladder costs an
+// LDS-crossbar round trip per step.)
+__device__ inline int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
 // Exclusive scan over the 256 digits of two values at once (digit = tid for
 // threads 0..255; wtot holds 2 x 4 wave totals).  Every thread of the
 // workgroup calls it (it contains a barrier); waves past the fourth pass
 // zeros and their results are unused.  Returns the exclusive prefixes.
-__device__ inline int2 scan256x2(int a, int c, int* wtot, int tid) {
+// drain: every thread first waits for its outstanding global memory
+// operations, so that they are complete once the barrier is passed.
+__device__ inline int2 scan256x2(int a, int c, int* wtot, int tid,
+                                 bool drain = false) {
   const int lane = tid & 63, wave = tid >> 6;
-  int ia = a, ic = c;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int ua = __shfl_up(ia, off, 64);
-    const int uc = __shfl_up(ic, off, 64);
-    if (lane >= off) {
-      ia += ua;
-      ic += uc;
-    }
-  }
+  const int ia = wave_incl_scan(a), ic = wave_incl_scan(c);
   if (lane == 63 && wave < 4) {
     wtot[wave] = ia;
     wtot[4 + wave] = ic;
   }
+  if (drain) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   int ba = 0, bc = 0;
   for (int w = 0; w < min(wave, 4); ++w) {
@@ -347,16 +357,21 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const bool valid = base + c * 64 + lane < N;
-    const uint32_t key = sort_key(kk[c], K);
-    const uint32_t d = (key >> shift) & dmask;
+    const uint32_t d = (sort_key(kk[c], K) >> shift) & dmask;
     unsigned long long* w = &lmask[wave][d];
     __hip_atomic_fetch_or(w, valid ? mybit : 0ull, __ATOMIC_RELAXED,
                           __HIP_MEMORY_SCOPE_WORKGROUP);
-    const uint64_t m = __hip_atomic_load(w, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_WORKGROUP);
+    match[c] = __hip_atomic_load(w, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
     __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    match[c] = m;
     dig[c] = (int)d;
+  }
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const bool valid = base + c * 64 + lane < N;
+    const uint32_t key = sort_key(kk[c], K);
+    const uint32_t d = (uint32_t)dig[c];
+    const uint64_t m = match[c];
     int o = 0;
     if (valid && lanes_below(m) == 0) o = atomicAdd(&cnt[wave][d], __popcll(m));
     lead[c] = o;
@@ -370,11 +385,13 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   // first lane.
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const bool valid = base + c * 64 + lane < N;
     const uint64_t m = match[c];
-    const int src = m ? (int)__builtin_ctzll(m) : lane;
-    const int old = __shfl(lead[c], src, 64);
-    rank[c] = valid ? old + (int)lanes_below(m) : -1;
+    lead[c] = __shfl(lead[c], m ? (int)__builtin_ctzll(m) : lane, 64);
+  }
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const bool valid = base + c * 64 + lane < N;
+    rank[c] = (lead[c] + (int)lanes_below(match[c])) | (valid ? 0 : -1);
   }
   __syncthreads();
 
@@ -404,11 +421,6 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
         const int v = hx[p - 1][tid];
         if (v) atomicAdd(grow + p * 256 + tid, v);
       }
-      // The adds are agent-scope atomics, performed where every workgroup
-      // reads them; waiting for their completion orders them before the
-      // arrival below (a release fence would also write back this XCD's L2,
-      // which cost ~0.1 us per wave).
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
   }
   // The first tile of a fused row clears the other phase's counts (used by
@@ -416,8 +428,12 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
   if (fuse && tile == 0)
     for (int i = tid; i < MAXP * 256; i += ST)
       a.gnext[(size_t)b * MAXP * 256 + i] = 0;
-  // Tile-local and global exclusive digit prefixes.
-  const int2 pre = scan256x2(total, gc, wtot, tid);
+  // Tile-local and global exclusive digit prefixes.  A fused pass's adds
+  // are agent-scope atomics, performed where every workgroup reads them;
+  // waiting for their completion (drain) before the scan's barrier orders
+  // them before the arrival below (a release fence would also write back
+  // this XCD's L2, which cost ~0.1 us per wave).
+  const int2 pre = scan256x2(total, gc, wtot, tid, fuse);
   if (fuse && tid == 0)
     __hip_atomic_fetch_add(crow + CTR_ARRIVE, 1ull, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -626,26 +642,37 @@ __global__ void __launch_bounds__(ST) sort_onesweep_kernel(SweepArgs a) {
     const int2 g = scan256x2(gc, 0, wtot, tid);
     if (tid < nb) gbase[tid] += g.x;
   }
+  // Placement in tile order, without branches so that every chunk's LDS
+  // reads are in flight at once: a key past N (only in a short last tile)
+  // goes to slot TILE - 1, which is at or past tn and never read.
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    if (rank[c] >= 0) {
-      const int pos = dstart[dig[c]] + cnt[wave][dig[c]] + rank[c];
-      skey[pos] = kk[c];
-      sval[pos] = vb ? vv[c] : base + c * 64 + lane;
-    }
+    const int d = dig[c];
+    const int pos =
+        rank[c] >= 0 ? dstart[d] + cnt[wave][d] + rank[c] : TILE - 1;
+    skey[pos] = kk[c];
+    sval[pos] = vb ? vv[c] : base + c * 64 + lane;
   }
   __syncthreads();
   int32_t* ko = a.keys_out + (size_t)b * N;
   int32_t* vo = a.vals_out + (size_t)b * N;
+  // Copy out: every slot is read (in LDS bounds; a slot past tn yields some
+  // digit in range) and only the stores are masked.
+  constexpr int PER_T = TILE / ST;
+  int32_t ok[PER_T], ov[PER_T], op[PER_T];
 #pragma unroll
-  for (int j = 0; j < TILE / ST; ++j) {
-    const int i = tid + j * ST;
-    if (i < tn) {
-      const int32_t key = skey[i];
-      const int d = (int)((sort_key(key, K) >> shift) & dmask);
-      const int pos = gbase[d] + i;
-      ko[pos] = key;
-      vo[pos] = sval[i];
+  for (int j = 0; j < PER_T; ++j) {
+    ok[j] = skey[tid + j * ST];
+    ov[j] = sval[tid + j * ST];
+  }
+#pragma unroll
+  for (int j = 0; j < PER_T; ++j)
+    op[j] = gbase[(sort_key(ok[j], K) >> shift) & dmask] + tid + j * ST;
+#pragma unroll
+  for (int j = 0; j < PER_T; ++j) {
+    if (tid + j * ST < tn) {
+      ko[op[j]] = ok[j];
+      vo[op[j]] = ov[j];
     }
   }
 }
