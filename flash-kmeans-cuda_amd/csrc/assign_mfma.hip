@@ -172,6 +172,25 @@ __device__ inline void fold_saved(const f32x4& acc, float& best, int& bblk,
   best = nb;
 }
 
+// Issue priority by progress: 3 in the first quarter of a workgroup's
+// stages, then 2, 1, 0.  Two workgroups share each SIMD of a CU, and the
+// arbiter prefers the older wave: without this the one that started first
+// ran ahead (c3: its loop 44 us against 57 us for its partner on every CU;
+// c5: 266 against 392 us) and the other finished alone, one wave per SIMD
+// with nothing to hide its latency.  With priority falling as a workgroup
+// advances, the one behind wins arbitration, so the pair stays level.
+__device__ inline void progress_prio(int done, int total) {
+  const int q = (4 * done) / total;  // 0..3 while done < total
+  if (q == 0)
+    __builtin_amdgcn_s_setprio(3);
+  else if (q == 1)
+    __builtin_amdgcn_s_setprio(2);
+  else if (q == 2)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // DS2: 32-feature steps (padded width DP = 32*DS2 >= D); PT: 16-point tiles
 // per wave; PAD: D < DP, so segments past D read as zeros (a compile-time
 // flag: the unpadded variants carry no per-load condition); EXACT: track
@@ -478,6 +497,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     fixq(0, s_q0);
     __syncthreads();
     for (int chunk = 0; chunk < nch; chunk += 2) {
+      progress_prio(chunk, nch);
       if (chunk + 1 < nch) issue(chunk + 1, s_c1, s_q1);
       compute(chunk, s_c0, s_q0);
       __builtin_amdgcn_sched_barrier(0);
@@ -537,6 +557,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
 
     for (int chunk = 0; chunk < nchunks; ++chunk) {
       const int buf = chunk & 1;
+      progress_prio(chunk, nchunks);
       if (chunk + 1 < nchunks) gload(chunk + 1);
       const uint16_t* lc = lds_c[buf];
       const float* lq = lds_q[buf];
