@@ -461,6 +461,22 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     starts[c] = __builtin_amdgcn_ballot_w64(p < p1 && ivs[c] != before);
   }
 
+  // Per chunk, each lane's row of the gather: its byte offset in the batch
+  // row (row 0's where the row is past the unit or its permutation entry is
+  // outside [0,N): read but not folded) and the ballot of rows folded.
+  uint64_t goff[CH];
+  uint64_t gok[CH];
+  const char* xl[NI];  // this lane's column of row 0
+#pragma unroll
+  for (int i = 0; i < NI; ++i) xl[i] = reinterpret_cast<const char*>(xb + lcol[i]);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int p = p0 + c * 64 + lane;
+    const bool ok = p < p1 && (uint32_t)pvs[c] < (uint32_t)N;
+    goff[c] = (uint64_t)(uint32_t)(ok ? pvs[c] : 0) * (uint64_t)D * sizeof(T);
+    gok[c] = __builtin_amdgcn_ballot_w64(ok);
+  }
+
   int cur = __builtin_amdgcn_readfirstlane(ivs[0]);
   int rs = p0;
   if (overwrite && !fused && !(has_prev && prev == cur))
@@ -497,22 +513,26 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
     const int r0 = q * RB;  // first unit row of the batch
     if (r0 >= urows) break;
     R raw[RB][NI];
-    uint32_t okm = 0;  // rows with a permutation entry in [0,N) inside the unit
+    // Rows with a permutation entry in [0,N) inside the unit (bit jj: row
+    // r0 + jj), from the chunk's ballot.
+    const uint32_t okm =
+        (uint32_t)(gok[r0 >> 6] >> (r0 & 63)) & (RB == 32 ? ~0u : (1u << RB) - 1u);
 #pragma unroll
     for (int jj = 0; jj < RB; ++jj) {
-      const int r = r0 + jj;
-      const int rr = min(r, urows - 1);
-      const int row = __builtin_amdgcn_readlane(rr < 64 ? pvs[0] : pvs[CH - 1], rr & 63);
-      // A permutation entry outside [0,N), or a row past the unit, reads
-      // row 0 and is not folded.
-      const bool rok = r < urows && (uint32_t)row < (uint32_t)N;
-      okm |= rok ? (1u << jj) : 0u;
-      const T* xr = xb + (size_t)(rok ? row : 0) * D;
+      const int r = r0 + jj;  // a constant once unrolled
+      // The row's byte offset, held by lane r % 64 of its chunk: two lane
+      // reads, no per-row scalar arithmetic.
+      const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane(
+          (int)(uint32_t)goff[r >> 6], r & 63);
+      const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(
+          (int)(uint32_t)(goff[r >> 6] >> 32), r & 63);
+      const uint64_t off = (hi << 32) | lo;
       // Unconditional, from an in-bounds column: a lane past D loads column
       // 0 and its sums are never stored (every store checks cok), so no
       // per-row branch on the lane's column is needed.
 #pragma unroll
-      for (int i = 0; i < NI; ++i) raw[jj][i] = RC::load(xr + lcol[i]);
+      for (int i = 0; i < NI; ++i)
+        raw[jj][i] = RC::load(reinterpret_cast<const T*>(xl[i] + off));
     }
 #pragma unroll
     for (int h = 0; h < RB / FH; ++h) {
