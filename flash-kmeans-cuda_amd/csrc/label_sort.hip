@@ -712,14 +712,17 @@ SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
   // 9.8 at 131072 and 12.0 / 10.4 / 9.6 at 8 x 65536), and up to 32768
   // keys 512-key tiles shorten it once more (Lloyd loop, us per iteration
   // with 512 / 1024-key tiles: 30.8-31.1 / 31.9-32.6 at 4096 keys, 30.0-30.2
-  // / 30.3-30.7 at 32768; at 65536 they lose 2.5 us).  Batches of short
+  // / 30.3-30.7 at 32768; at 65536 they lose 2.5 us).  With the ranking by
+  // LDS lane masks a tile's own work is cheaper, and the balance moved:
+  // 1024-key tiles at 32768 keys (27.5-28.2 against 28.3-28.8 us; 256-key
+  // tiles at 4096 keys were within noise).  Batches of short
   // rows take 2048-key tiles when a row needs at most 32 of them and the
   // grid stays resident: the chain stays short and each tile's own work
   // halves (8 x 65536 keys: 118.8-119.3 against 120.2-120.3 us per
   // iteration; with longer chains 2048 loses: 1 x 131072 +1 us, 1 x 524288
   // +5 us).  FKC_SORT_TILE overrides.
   const int64_t t2k = (N + 2047) / 2048;
-  int tile = B * N <= 32768   ? 512
+  int tile = B * N <= 16384   ? 512
              : B * N <= 65536 ? 1024
              : (B > 1 && t2k <= 32 && B * t2k <= STATIC_TILES_MAX) ? 2048
                               : 4096;
