@@ -21,8 +21,9 @@
 //   sort_upsweep  : (larger grids) one read of the keys counts the digits of
 //                   every pass into the global counts before the passes.
 //   sort_onesweep : ranks its tile's keys stably by digit (per 64-key chunk,
-//                   one ballot per digit bit gives every lane the mask of
-//                   lanes holding its digit, "multi-split"), publishes its
+//                   every lane ORs its lane bit into the wave's LDS word for
+//                   its digit and reads the word back: the mask of lanes
+//                   holding its digit, "multi-split"), publishes its
 //                   per-digit counts, then walks back over earlier tiles'
 //                   status words, adding their counts until it meets an
 //                   inclusive prefix, and publishes its own inclusive prefix.
