@@ -45,6 +45,11 @@
 // 16 bytes.
 // Centroid rows past K re-read row K-1 instead of branching (their scores
 // are masked to -inf).
+// Where a batch row's whole centroid table fits one workgroup's LDS (D = 32
+// and 64, K up to 2400 / 1216) and the grid gives every CU a workgroup,
+// assign_resident_kernel loads the table once per workgroup and its 16
+// waves walk their point tiles against it with no barrier in the loop; its
+// scores and fold are the same, so its labels are identical.
 #include "device_util.hpp"
 #include "fkc_internal.hpp"
 
@@ -758,6 +763,297 @@ assign_merge_kernel(const float* __restrict__ psc,
   ids[b * N + n] = bi;
 }
 
+// ------------------------------------------------------------------------
+// Centroid-resident variant.  When a batch row's whole centroid table fits
+// in one workgroup's LDS (Kp = K rounded up to 32 rows of DP features, plus
+// Kp scaled c_sq values: resident_bytes(Kp) <= kResidentLds, i.e. K <= 1216
+// at D = 64 and K <= 2400 at D = 32), each workgroup loads the table once
+// and its waves then walk their 16*PT-point tiles against it on their own:
+// no stage loads or barriers in the loop, the winner's candidate rows are
+// scored again from LDS rather than L2, and a wave that is loading its next
+// points or settling its labels leaves the matrix core to the other waves
+// of its SIMD instead of idling it for a whole round of workgroups.  The
+// scores are the same MFMA chains with the same seeds as the staged kernel,
+// folded by the same block rule and re-score, so the labels are identical.
+constexpr int kCUs = 256;                 // MI355X compute units
+constexpr int kResidentLds = 160 * 1024;  // LDS one workgroup may hold (gfx950)
+constexpr int kResidentWaves = 16;        // waves per workgroup (4 per SIMD)
+
+__host__ __device__ constexpr int resident_bytes(int ds2, int Kp) {
+  return Kp * (ds2 * 64 + 4);
+}
+
+// W waves per workgroup, PT tiles per wave: 16 x 8 at D = 32 (a block's
+// fragment read then feeds eight MFMAs, as at D = 64 with four) and 16 x 4
+// at D = 64, both within 128 VGPRs (4 waves per SIMD).  Measured at
+// (8, 65536, 1024, 64) bf16 against the staged kernel's 0.067-0.070 ms:
+// 0.063 ms (the loop unrolled by two so the fragment and accumulator sets
+// rotate without copies; 0.076 with a copy per block), progress priorities
+// 4.6% fewer cycles (matrix core busy 46.8 -> 49.1%, 2.59 -> 3.06 waves
+// resident per SIMD).  Eight tiles on eight waves at D = 64 (half the
+// fragment reads per MFMA at 2 waves per SIMD) and issue priorities
+// staggered over a SIMD's waves measured no faster.
+template <int DT, int DS2, int PT, int W>
+__global__ void __launch_bounds__(W * 64, 1)
+assign_resident_kernel(const uint16_t* __restrict__ x,
+                       const uint16_t* __restrict__ cent,
+                       const float* __restrict__ c_sq,
+                       int32_t* __restrict__ ids, int N, int K,
+                       const int32_t* __restrict__ ctrl) {
+  if (loop_done(ctrl)) return;
+  constexpr int DP = DS2 * 32;
+  constexpr int ROWB = DP * 2;
+  constexpr int SEGS = DP / 8;
+  constexpr int NTH = W * 64;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t s_res[];
+  const int Kp = (K + 31) & ~31;
+  uint8_t* lc = s_res;
+  float* lq = reinterpret_cast<float*>(s_res + (size_t)Kp * ROWB);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, g = lane >> 4;
+  const int b = blockIdx.y;
+  const uint16_t* xb = x + (size_t)b * N * DP;
+  const uint16_t* cb = cent + (size_t)b * K * DP;
+  const float* qb = c_sq + (size_t)b * K;
+
+  // This wave's first point tile is loaded before the table fill, so its
+  // HBM round trip overlaps the fill's.  Points past N load point N-1
+  // (their labels are not stored).
+  const int ntiles = (N + 16 * PT - 1) / (16 * PT);
+  int ts = blockIdx.x * W + wave;
+  u32x4 xr[PT][DS2];
+  auto load_points = [&](int tile) {
+    const int n0 = min(tile, ntiles - 1) * 16 * PT;
+#pragma unroll
+    for (int p = 0; p < PT; ++p) {
+      const int n = min(n0 + 16 * p + col, N - 1);
+      const u32x4* src = reinterpret_cast<const u32x4*>(xb + (size_t)n * DP);
+#pragma unroll
+      for (int s = 0; s < DS2; ++s) xr[p][s] = src[4 * s + g];
+    }
+  };
+  load_points(ts);
+
+  // Table fill, CH 16-byte loads in flight per thread.  Row r keeps feature
+  // segment v in slot v ^ swz(r), so a fragment read (16 consecutive rows)
+  // touches 16 distinct bank groups; rows K..Kp-1 repeat row K-1 and get
+  // the seed -inf, so they never win.
+  {
+    constexpr int CH = 8;
+    const int total = Kp * SEGS;
+    for (int i0 = 0; i0 < total; i0 += NTH * CH) {
+      u32x4 v[CH];
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int i = min(i0 + j * NTH + tid, total - 1);
+        const int r = i / SEGS, s = i % SEGS;
+        v[j] = *reinterpret_cast<const u32x4*>(cb + (size_t)min(r, K - 1) * DP +
+                                               s * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int i = i0 + j * NTH + tid;
+        if (i < total) {
+          const int r = i / SEGS, s = i % SEGS;
+          *reinterpret_cast<u32x4*>(lc + r * ROWB + ((s ^ swz<SEGS>(r)) * 16)) =
+              v[j];
+        }
+      }
+    }
+    for (int k = tid; k < Kp; k += NTH) lq[k] = k < K ? -0.5f * qb[k] : -INFINITY;
+  }
+  __syncthreads();
+
+  const int nblk = Kp >> 4;
+  const int sw = swz<SEGS>(col);  // rows 16t + col share it
+  auto frag = [&](int t, u32x4* a, f32x4& ci) {
+    ci = *reinterpret_cast<const f32x4*>(lq + 16 * t + 4 * g);
+    const uint8_t* arow = lc + (16 * t + col) * ROWB;
+#pragma unroll
+    for (int s = 0; s < DS2; ++s)
+      a[s] = *reinterpret_cast<const u32x4*>(arow + (((4 * s + g) ^ sw) * 16));
+  };
+
+  // Point tiles of this batch row, strided over the row's waves; the next
+  // tile's points are loaded once this one's are no longer needed.
+  // Issue priority by progress, in halves of each tile: the arbiter
+  // prefers older waves, so without it the first waves of a SIMD finish
+  // early and the last run alone with nothing to hide their latency; with
+  // priority falling as a wave advances, the ones behind catch up.
+  const int stride = gridDim.x * W;
+  const int mine = ts < ntiles ? (ntiles - ts + stride - 1) / stride : 1;
+  for (int k = 0; ts < ntiles; ts += stride, ++k) {
+    const int n0 = ts * 16 * PT;
+    progress_prio(2 * k, 2 * mine);
+    float best[PT];
+    int bblk[PT];
+#pragma unroll
+    for (int p = 0; p < PT; ++p) {
+      best[p] = -INFINITY;
+      bblk[p] = 0;
+    }
+    // Two blocks per trip with ping-pong registers (no copies): block t's
+    // MFMAs run while block t+1's fragments are read and block t-1 is
+    // folded; the table has an even number of blocks (Kp % 32 == 0).  The
+    // fold of the -inf seed before block 0 changes nothing, and the read
+    // past the last block re-reads block 0.  Eight tiles have no registers
+    // for a second accumulator set: each block is folded after its own
+    // MFMAs (the other waves of the SIMD cover the wait).
+    u32x4 a0[DS2], a1[DS2];
+    f32x4 c0, c1;
+    f32x4 accA[PT], accB[PT];
+#pragma unroll
+    for (int p = 0; p < PT; ++p)
+      accB[p] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    auto chain = [&](const u32x4* a, const f32x4& ci, f32x4* acc) {
+#pragma unroll
+      for (int s = 0; s < DS2; ++s) {
+#pragma unroll
+        for (int p = 0; p < PT; ++p)
+          acc[p] = mfma16<DT>(a[s], xr[p][s], s == 0 ? ci : acc[p]);
+      }
+    };
+    auto fold = [&](const f32x4* acc, int blk) {
+#pragma unroll
+      for (int p = 0; p < PT; ++p) fold_block(acc[p], best[p], bblk[p], blk);
+    };
+    auto hint = [&]() {
+      if constexpr (FKC_SCHED_GROUPS && PT < 8) {
+        __builtin_amdgcn_sched_group_barrier(0x100, DS2 + 1, 0);  // LDS reads
+#pragma unroll
+        for (int i = 0; i < DS2 * PT; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        }
+      }
+    };
+    frag(0, a0, c0);
+    for (int t = 0; t < nblk; t += 2) {
+      if (t == (nblk >> 2) * 2) progress_prio(2 * k + 1, 2 * mine);
+      frag(t + 1, a1, c1);
+      chain(a0, c0, accA);
+      if constexpr (PT >= 8)
+        fold(accA, 16 * t);
+      else
+        fold(accB, 16 * (t - 1));
+      hint();
+      frag(t + 2 < nblk ? t + 2 : 0, a0, c0);
+      chain(a1, c1, accB);
+      if constexpr (PT >= 8)
+        fold(accB, 16 * (t + 1));
+      else
+        fold(accA, 16 * t);
+      hint();
+    }
+    if constexpr (PT < 8) fold(accB, 16 * (nblk - 1));
+
+    // Settle each point as the staged kernel does (higher score, ties to
+    // the lower candidate base; then the first of the four candidate rows
+    // reaching the maximum of the re-scored diagonal), with the candidate
+    // rows and seeds read from the LDS table.  base + r < Kp always.
+    const int e = col & 3;
+#pragma unroll
+    for (int p = 0; p < PT; ++p) {
+      float bv = best[p];
+      int base = bblk[p] + 4 * g;
+#pragma unroll
+      for (int off = 16; off <= 32; off <<= 1) {
+        const float ob = __shfl_xor(bv, off, 64);
+        const int obase = __shfl_xor(base, off, 64);
+        if (ob > bv || (ob == bv && obase < base)) {
+          bv = ob;
+          base = obase;
+        }
+      }
+      float dv[4];
+      const f32x4 seeds = *reinterpret_cast<const f32x4*>(lq + base);  // base % 4 == 0
+      // Candidate rows from the table (their random rows cost LDS bank
+      // conflicts, ~10 cycles per read at c4's shape, but reading them from
+      // L2 instead, as the staged kernel does, measured 6% slower there).
+      u32x4 ar[4][DS2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kr = base + r;
+        const uint8_t* crow = lc + kr * ROWB;
+        const int ksw = swz<SEGS>(kr);
+#pragma unroll
+        for (int s = 0; s < DS2; ++s)
+          ar[r][s] = *reinterpret_cast<const u32x4*>(crow + (((4 * s + g) ^ ksw) * 16));
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float seed = seeds[r];
+        f32x4 acc = {seed, seed, seed, seed};
+#pragma unroll
+        for (int s = 0; s < DS2; ++s) acc = mfma16<DT>(ar[r][s], xr[p][s], acc);
+        float d = acc[0];
+        d = e == 1 ? acc[1] : d;
+        d = e == 2 ? acc[2] : d;
+        d = e == 3 ? acc[3] : d;
+        dv[r] = d;
+      }
+      int rr = 0;
+      float m = dv[0];
+#pragma unroll
+      for (int r = 1; r < 4; ++r) {
+        if (dv[r] > m) {
+          m = dv[r];
+          rr = r;
+        }
+      }
+      const int n = n0 + 16 * p + col;
+      if (g == (col >> 2) && n < N) ids[(size_t)b * N + n] = base + rr;
+    }
+    if (ts + stride < ntiles) load_points(ts + stride);
+  }
+}
+
+// Workgroups per batch row of a resident launch: one round of the chip
+// (workgroups per CU set by the table's LDS), no more than the row's tiles
+// need.
+static int64_t resident_need(int pt, int w, int64_t N) {
+  const int64_t tiles = (N + 16 * pt - 1) / (16 * pt);
+  return (tiles + w - 1) / w;
+}
+
+static int resident_grid(int pt, int w, int64_t B, int64_t N) {
+  const int64_t fill = std::max<int64_t>(1, kCUs / B);
+  return (int)std::max<int64_t>(1, std::min(resident_need(pt, w, N), fill));
+}
+
+template <int DT, int DS2, int PT, int W>
+int launch_resident_t(const void* x, const void* c, const float* c_sq,
+                      int32_t* ids, int64_t B, int64_t N, int64_t K,
+                      const int32_t* ctrl, hipStream_t s, hipEvent_t ev0,
+                      hipEvent_t ev1) {
+  // Dynamic LDS above the default limit needs the kernel's attribute raised
+  // once per process.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&assign_resident_kernel<DT, DS2, PT, W>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kResidentLds);
+  if (attr != hipSuccess)
+    return fail(FKC_ERR_LAUNCH, "assign_resident: LDS attribute: %s",
+                hipGetErrorString(attr));
+  const int Kp = (int)((K + 31) & ~31);
+  const size_t lds = (size_t)resident_bytes(DS2, Kp);
+  dim3 grid((unsigned)resident_grid(PT, W, B, N), (unsigned)B);
+  if (ev0 != nullptr)
+    hipExtLaunchKernelGGL((assign_resident_kernel<DT, DS2, PT, W>), grid,
+                          dim3(W * 64), lds, s, ev0, ev1, 0,
+                          static_cast<const uint16_t*>(x),
+                          static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
+                          (int)K, ctrl);
+  else
+    hipLaunchKernelGGL((assign_resident_kernel<DT, DS2, PT, W>), grid,
+                       dim3(W * 64), lds, s,
+                       static_cast<const uint16_t*>(x),
+                       static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
+                       (int)K, ctrl);
+  return check_launch("assign_resident");
+}
+
 // Centroid slicing of one launch: S slices of kspan rows (S = 1: none);
 // psc / pidx hold B x S x N partial winners when S > 1.
 struct Slices {
@@ -917,6 +1213,7 @@ static int choose_pt(int ds2, bool pad, bool exact, int64_t B, int64_t N) {
 struct Plan {
   int ds2, pt, S, kspan;
   bool pad, exact, save;
+  bool resident = false;  // assign_resident_kernel (pt: its tiles per wave)
 };
 
 // The saved-score fold keeps the best block's four scores per lane, so the
@@ -936,6 +1233,26 @@ static bool use_save(const Plan& p, int64_t wgs) {
   const int o = save_override();
   if (o >= 0) return o == 1;
   return p.ds2 == 4 ? wgs <= 512 : p.kspan <= 1024;
+}
+
+// Tiles per wave of the resident kernel.
+static int resident_pt(int ds2) { return ds2 == 1 ? 8 : 4; }
+
+// The centroid-resident kernel: unpadded D = 32 or 64 whose centroid table
+// fits one workgroup's LDS.  Taken where its grid gives every CU a
+// workgroup and K is past the exact-index cutoff (measured: fewer
+// workgroups than CUs leave the table fill and the first point loads
+// unhidden, and at small K the staged kernel's exact fold is as fast).
+// FKC_RESIDENT=0/1 forces it off / on where the table fits.
+static bool use_resident(const Plan& p, int64_t B, int64_t N, int64_t K) {
+  if (p.pad || (p.ds2 != 1 && p.ds2 != 2)) return false;
+  const int64_t Kp = (K + 31) & ~int64_t{31};
+  if (Kp * (p.ds2 * 64 + 4) > kResidentLds) return false;
+  const int o = resident_override();
+  if (o >= 0) return o == 1;
+  const int pt = resident_pt(p.ds2);
+  return K > FKC_EXACT_MAX_K_NARROW &&
+         B * resident_need(pt, kResidentWaves, N) >= kCUs;
 }
 
 // Launch plan.  K is sliced only when no unsliced grid fills the chip (few
@@ -967,6 +1284,13 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   p.pt = choose_pt(p.ds2, p.pad, p.exact, B, N);
   p.S = 1;
   p.kspan = (int)K;
+  if (use_resident(p, B, N, K)) {
+    p.resident = true;
+    p.exact = false;
+    p.save = false;
+    p.pt = resident_pt(p.ds2);
+    return p;
+  }
   p.save = use_save(p, grid_wgs(p.pt, B, N));
   if (!can_slice || p.exact) return p;
   // Four tiles, not eight: on sliced-size grids four tiles on ~256
@@ -1032,6 +1356,18 @@ int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                        hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
                        void* ws, size_t ws_bytes) {
   const Plan p = plan_assign(B, N, K, D, ws != nullptr);
+  if (p.resident) {
+    using RL = int (*)(const void*, const void*, const float*, int32_t*,
+                       int64_t, int64_t, int64_t, const int32_t*, hipStream_t,
+                       hipEvent_t, hipEvent_t);
+    constexpr int W = kResidentWaves;
+    const bool f16 = dtype == FKC_F16;
+    RL fn = p.ds2 == 1 ? (f16 ? &launch_resident_t<FKC_F16, 1, 8, W>
+                              : &launch_resident_t<FKC_BF16, 1, 8, W>)
+                       : (f16 ? &launch_resident_t<FKC_F16, 2, 4, W>
+                              : &launch_resident_t<FKC_BF16, 2, 4, W>);
+    return fn(x, c, c_sq, ids, B, N, K, ctrl, s, ev0, ev1);
+  }
   Slices sl;
   const size_t need = slice_bytes(p, B, N, &sl, ws);
   if (need > ws_bytes)

@@ -72,6 +72,12 @@ int save_override() {
   return std::strcmp(s, "1") == 0 ? 1 : (std::strcmp(s, "0") == 0 ? 0 : -1);
 }
 
+int resident_override() {
+  const char* s = std::getenv("FKC_RESIDENT");
+  if (!s || !*s) return -1;
+  return std::strcmp(s, "1") == 0 ? 1 : (std::strcmp(s, "0") == 0 ? 0 : -1);
+}
+
 bool sort_fuse_override() {
   const char* s = std::getenv("FKC_SORT_FUSE");
   return !(s && std::strcmp(s, "0") == 0);

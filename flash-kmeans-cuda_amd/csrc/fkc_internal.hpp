@@ -194,5 +194,8 @@ int ksplit_override();
 // FKC_SAVE=0|1: saved-score fold of the four-tile D = 97..128 assign off /
 // on where it exists; -1 = auto.
 int save_override();
+// FKC_RESIDENT=0|1: centroid-resident assign off / on where the table fits
+// in LDS; -1 = auto.
+int resident_override();
 
 }  // namespace fkc

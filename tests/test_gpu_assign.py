@@ -146,6 +146,50 @@ def test_eight_tiles_match_oracle_and_four(monkeypatch, dtype, B, N, K):
     _check(x, c, dtype, got8, max_frac=1e-3)
 
 
+RESIDENT_CASES = [
+    # (B, N, K, D): one centroid, K below and not a multiple of 16, ragged N,
+    # batches, c4's shape at reduced N, and the largest tables that fit one
+    # workgroup's LDS (K = 1216 at D = 64, 2400 at D = 32).
+    (1, 1000, 1, 64), (1, 777, 13, 64), (2, 3001, 100, 32), (3, 999, 517, 64),
+    (8, 4096, 1024, 64), (1, 5000, 1216, 64), (1, 3000, 2400, 32),
+    (1, 70000, 600, 32),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("B,N,K,D", RESIDENT_CASES)
+def test_resident_table_matches_staged_and_oracle(monkeypatch, dtype, B, N, K, D):
+    """The centroid-resident kernel (whole table in LDS, waves walking their
+    point tiles without barriers) against the oracle and, bit for bit,
+    against the staged kernel on the same shape."""
+    x, c = _data(B, N, K, D, dtype, seed=7 * N + K + D)
+    monkeypatch.setenv("FKC_RESIDENT", "1")
+    got_r = _gpu_assign(x, c, dtype)
+    monkeypatch.setenv("FKC_RESIDENT", "0")
+    got_s = _gpu_assign(x, c, dtype)
+    assert np.array_equal(got_r, got_s)
+    _check(x, c, dtype, got_r, max_frac=1e-3 if B * N >= 4096 else None)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_resident_table_ties_and_identity(monkeypatch, dtype):
+    """Duplicate centroids take the lowest index and the first K points as
+    centroids map to themselves on the resident kernel, including across
+    the 16-row blocks and the last partial block."""
+    monkeypatch.setenv("FKC_RESIDENT", "1")
+    x, c = _data(2, 4000, 300, 64, dtype, seed=19)
+    c[:, 299] = c[:, 3]
+    c[:, 17] = c[:, 16]
+    c[:, 200] = c[:, 31]
+    got = _gpu_assign(x, c, dtype)
+    assert not np.isin(got, [299, 17, 200]).any()
+    _check(x, c, dtype, got)
+    x, _ = _data(1, 5000, 1, 32, dtype, seed=23)
+    c = x[:, :1100].copy()
+    got = _gpu_assign(x, c, dtype)
+    assert np.array_equal(got[0, :1100], np.arange(1100))
+
+
 SLICE_CASES = [
     # (B, N, K, D, dtype, FKC_KSPLIT or None for the automatic plan)
     (1, 5000, 4096, 128, "f16", None),     # 2 slices of 2048 rows
