@@ -363,6 +363,33 @@ def test_loop_with_sliced_assign(monkeypatch, B, N, K, dtype):
         assert torch.equal(a[0], r[0]) and torch.equal(a[1], r[1])
 
 
+@pytest.mark.parametrize("B,N,K,D,dtype,tol", [
+    (8, 65536, 1024, 64, "bf16", 0.0),    # c4's shape: resident by default
+    (2, 40000, 700, 64, "bf16", 1e-4),    # forced resident, tol stop
+    (1, 30000, 2000, 32, "f16", 0.0),     # D = 32, eight tiles per wave
+])
+def test_loop_with_resident_assign(monkeypatch, B, N, K, D, dtype, tol):
+    """The Lloyd loop with the centroid-resident assign forced on and off:
+    labels, centroids and iteration count equal bit for bit (clustered data,
+    so the loop moves the centroids and reassigns points)."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    rng = np.random.default_rng(N + K)
+    centers = rng.standard_normal((B, 64, D)).astype(np.float32) * 3.0
+    pick = rng.integers(0, 64, (B, N))
+    pts = np.take_along_axis(centers, pick[..., None], axis=1)
+    pts = pts + rng.standard_normal((B, N, D)).astype(np.float32)
+    x = O.from_f32(pts, dtype)
+    init = np.ascontiguousarray(x[:, :K])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    runs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("FKC_RESIDENT", flag)
+        runs.append(batch_kmeans_Euclid(xt, K, max_iters=6, tol=tol, init_centroids=it))
+    (ia, ca, na), (ib, cb, nb) = runs
+    assert na == nb
+    assert torch.equal(ia, ib) and torch.equal(ca, cb)
+
+
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_init_kept_and_entry_points_agree(dtype):
     """batch_kmeans_Euclid never writes init_centroids (the copy is fused
