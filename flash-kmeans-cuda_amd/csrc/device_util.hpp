@@ -53,10 +53,13 @@ __device__ inline int wave_sum_i(int v) {
 // Row reductions of the norm / finalize kernels (row_sqnorm, finalize, the
 // finalize fused into the centroid update) all use one order, so their
 // results agree bit for bit: lane l covers the columns VEC*(l + 64*i) + v,
-// i = 0, 1, ..., v < VEC, with VEC = row_vec(D) (2 for even D, else 1),
+// i = 0, 1, ..., v < VEC, with VEC = row_vec(D) (2 for even D above 64,
+// else 1: a row of at most 64 columns then fills the wave's 64 lanes),
 // accumulated with fma in (i, v) order; the 64 lane partials are then added
 // by row_sum.  (The centroid update holds its sums in exactly this layout.)
-__host__ __device__ inline int row_vec(int D) { return (D & 1) ? 1 : 2; }
+__host__ __device__ inline int row_vec(int D) {
+  return ((D & 1) || D <= 64) ? 1 : 2;
+}
 
 // Sum of v over the 64 lanes by a fixed tree of DPP moves: pairs and quads
 // (quad_perm), 8-lane halves (row_half_mirror), 16-lane rows (row_mirror),

@@ -811,7 +811,7 @@ update_merge_kernel(const float* __restrict__ part,
 
 // Column slices per lane pass: VEC columns per lane (2 when D is even), NI
 // slices of 64 lanes per row (1, 2 or 4), and grid.z column blocks beyond.
-inline int runs_vec(int64_t D) { return D % 2 == 0 ? 2 : 1; }
+inline int runs_vec(int64_t D) { return row_vec((int)D); }
 inline int runs_ni(int64_t D) {
   const int64_t slices = (D + 64 * runs_vec(D) - 1) / (64 * runs_vec(D));
   return slices <= 1 ? 1 : (slices <= 2 ? 2 : 4);
