@@ -153,6 +153,8 @@ RESIDENT_CASES = [
     (1, 1000, 1, 64), (1, 777, 13, 64), (2, 3001, 100, 32), (3, 999, 517, 64),
     (8, 4096, 1024, 64), (1, 5000, 1216, 64), (1, 3000, 2400, 32),
     (1, 70000, 600, 32),
+    # one point, and fewer points than one wave's tile, per batch row
+    (1, 1, 100, 64), (3, 5, 1216, 64), (2, 70, 2400, 32),
 ]
 
 
