@@ -236,6 +236,153 @@ row_sqnorm_kernel(const typename Elem<DT>::T* __restrict__ src,
   if (lane == 0) out[row] = acc;
 }
 
+// Table-resident variant, for tables small enough to sit in LDS whole: the
+// K centroid rows and the workgroup's points (rows of D + 4 floats, so every
+// row is 16-byte aligned and the 16 lanes of a point read 16 distinct bank
+// groups) and the K c_sq values are loaded in one batched round trip, then
+// every lane runs its centroids' FMA chains with no further barrier.  The
+// chains (one lane per (point, centroid), feature order, starting from 0),
+// the distance expression, its clamp, the strict-< scan in rising k and the
+// lane merge are those of assign_valu_kernel, so the labels are the same.
+// Measured at c1 (1, 4096, 64, 128) fp32, same box: assign 0.0133 -> 0.0108
+// -0.0113 ms, Lloyd iteration 0.0332 -> 0.0282-0.0300 ms; a fill in one
+// batch of 16 loads per thread and a 4x unrolled feature loop changed
+// nothing (the kernel is a few dependent round trips at this size).
+constexpr int kValuResidentLds = 64 * 1024;
+
+__host__ __device__ inline int64_t valu_res_bytes(int64_t K, int64_t D,
+                                                  int ppw) {
+  return (K * (D + 4) + ppw * (D + 4) + K) * 4;
+}
+
+// Four consecutive elements (4-element aligned) as fp32.
+template <int DT>
+__device__ inline float4 load4(const typename Elem<DT>::T* p) {
+  using E = Elem<DT>;
+  if constexpr (DT == FKC_F32) {
+    return *reinterpret_cast<const float4*>(p);
+  } else {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    typename E::T e[4];
+    __builtin_memcpy(&e[0], &r, 8);
+    return float4{E::load(e[0]), E::load(e[1]), E::load(e[2]), E::load(e[3])};
+  }
+}
+
+template <int DT, int SPLIT>
+__global__ void __launch_bounds__(VT)
+assign_valu_resident_kernel(const typename Elem<DT>::T* __restrict__ x,
+                            const typename Elem<DT>::T* __restrict__ c,
+                            const float* __restrict__ x_sq,
+                            const float* __restrict__ c_sq,
+                            int32_t* __restrict__ ids, int N, int K, int D,
+                            const int32_t* __restrict__ ctrl) {
+  using T = typename Elem<DT>::T;
+  constexpr int PPW = VT / SPLIT;  // points per workgroup
+  constexpr int CH = 8;            // 16-byte loads in flight per thread
+  if (loop_done(ctrl)) return;
+  extern __shared__ __attribute__((aligned(16))) float s_vr[];
+  const int DP = D + 4;
+  float* tab = s_vr;              // K rows of DP
+  float* pts = tab + K * DP;      // PPW rows of DP
+  float* tq = pts + PPW * DP;     // K
+  const int tid = threadIdx.x;
+  const int sl = tid % SPLIT, pl = tid / SPLIT;
+  const int b = blockIdx.y;
+  const int n0 = blockIdx.x * PPW;
+  const int n = n0 + pl;
+  const T* cb = c + (size_t)b * K * D;
+  const T* xb = x + (size_t)b * N * D;
+
+  // Fill: every load of a batch is issued before any store.  Groups of four
+  // elements never cross a row (D % 4 == 0); points past N load row N-1.
+  const int qd = D / 4;
+  const int nt = K * qd, np = PPW * qd;
+  for (int i0 = 0; i0 < nt + np; i0 += VT * CH) {
+    float4 v[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int i = min(i0 + j * VT + tid, nt + np - 1);
+      if (i < nt) {
+        v[j] = load4<DT>(cb + (size_t)i * 4);
+      } else {
+        const int r = (i - nt) / qd, q = (i - nt) - r * qd;
+        v[j] = load4<DT>(xb + (size_t)min(n0 + r, N - 1) * D + q * 4);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int i = i0 + j * VT + tid;
+      if (i < nt) {
+        const int k = i / qd, q = i - k * qd;
+        *reinterpret_cast<float4*>(tab + k * DP + q * 4) = v[j];
+      } else if (i < nt + np) {
+        const int r = (i - nt) / qd, q = (i - nt) - r * qd;
+        *reinterpret_cast<float4*>(pts + r * DP + q * 4) = v[j];
+      }
+    }
+  }
+  for (int k = tid; k < K; k += VT) tq[k] = c_sq[(size_t)b * K + k];
+  __syncthreads();
+
+  const float* xp = pts + pl * DP;
+  float xs = 0.f;
+  if (x_sq != nullptr) {
+    xs = n < N ? x_sq[(size_t)b * N + n] : 0.f;
+  } else {
+    for (int d = 0; d < D; ++d) {
+      const float v = xp[d];
+      xs = fmaf(v, v, xs);
+    }
+  }
+  float best = FLT_MAX;
+  int bidx = 0;
+  constexpr int JB = 4;  // centroids scored together (x read once per 4)
+  const int kpl = (K - sl + SPLIT - 1) / SPLIT;  // k = sl + j * SPLIT
+  for (int j0 = 0; j0 < kpl; j0 += JB) {
+    float acc[JB];
+    const float* crow[JB];
+#pragma unroll
+    for (int jj = 0; jj < JB; ++jj) {
+      acc[jj] = 0.f;
+      crow[jj] = tab + min(sl + (j0 + jj) * SPLIT, K - 1) * DP;
+    }
+    for (int d = 0; d < D; d += 4) {
+      const float4 xv = *reinterpret_cast<const float4*>(xp + d);
+#pragma unroll
+      for (int jj = 0; jj < JB; ++jj) {
+        const float4 cv = *reinterpret_cast<const float4*>(crow[jj] + d);
+        acc[jj] = fmaf(xv.x, cv.x, acc[jj]);
+        acc[jj] = fmaf(xv.y, cv.y, acc[jj]);
+        acc[jj] = fmaf(xv.z, cv.z, acc[jj]);
+        acc[jj] = fmaf(xv.w, cv.w, acc[jj]);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < JB; ++jj) {
+      if (j0 + jj < kpl) {
+        const int k = sl + (j0 + jj) * SPLIT;
+        float dist = xs + tq[k] - 2.0f * acc[jj];
+        dist = dist > 0.f ? dist : 0.f;
+        if (dist < best) {  // k rises with j: the first minimum is kept
+          best = dist;
+          bidx = k;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < SPLIT; off <<= 1) {
+    const float ob = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(bidx, off, 64);
+    if (ob < best || (ob == best && oi < bidx)) {
+      best = ob;
+      bidx = oi;
+    }
+  }
+  if (n < N && sl == 0) ids[(size_t)b * N + n] = bidx;
+}
+
 // PREF (several lanes per point and D a multiple of the 32-feature chunk):
 // the prefetching step loop, measured at (1, 4096, 64, 128) fp32 0.0180 ->
 // 0.0129 ms and (1, 65536, 1024, 64) fp32 0.338 -> 0.308 ms.
@@ -247,6 +394,14 @@ int launch_valu_split(const void* x, const void* c, const float* x_sq,
   using T = typename Elem<DT>::T;
   constexpr int PPW = VT / SPLIT;
   dim3 grid((unsigned)((N + PPW - 1) / PPW), (unsigned)B);
+  const int64_t rbytes = valu_res_bytes(K, D, PPW);
+  if (D % 4 == 0 && rbytes <= kValuResidentLds && resident_override() != 0) {
+    hipLaunchKernelGGL((assign_valu_resident_kernel<DT, SPLIT>), grid,
+                       dim3(VT), (size_t)rbytes, s, static_cast<const T*>(x),
+                       static_cast<const T*>(c), x_sq, c_sq, ids, (int)N,
+                       (int)K, (int)D, ctrl);
+    return check_launch("assign_valu_resident");
+  }
   if (SPLIT > 1 && D % VDC == 0)
     hipLaunchKernelGGL((assign_valu_kernel<DT, SPLIT, SPLIT != 1>), grid,
                        dim3(VT), 0, s, static_cast<const T*>(x),

@@ -278,6 +278,29 @@ def test_fp16_odd_widths_use_fp32_route(D):
     assert np.array_equal(got, got2)
 
 
+@pytest.mark.parametrize("B,N,K,D,dtype", [
+    (1, 4096, 64, 128, "f32"),    # c1: sixteen lanes per point
+    (2, 1000, 100, 36, "f32"),    # D not a multiple of the 32-feature chunk
+    (1, 513, 1, 16, "f32"),       # one centroid
+    (3, 70, 10, 4, "f32"),        # fewer points than a workgroup holds
+    (1, 3000, 60, 44, "f16"),     # odd-width 16-bit rows on the fp32 route
+    (2, 777, 90, 52, "bf16"),
+])
+def test_valu_resident_table_matches_tiled(monkeypatch, B, N, K, D, dtype):
+    """The vector route's table-resident kernel (table and points loaded
+    into LDS once, no barrier after) against the tiled kernel bit for bit,
+    with x_sq passed and computed in the kernel, and against the oracle."""
+    x, c = _data(B, N, K, D, dtype, seed=N * 3 + K + D)
+    monkeypatch.setenv("FKC_RESIDENT", "1")
+    got_r = _gpu_assign(x, c, dtype)
+    got_r2 = _gpu_assign(x, c, dtype, with_xsq=False)
+    monkeypatch.setenv("FKC_RESIDENT", "0")
+    got_t = _gpu_assign(x, c, dtype)
+    assert np.array_equal(got_r, got_t)
+    assert np.array_equal(got_r2, got_t)
+    _check(x, c, dtype, got_r, max_frac=1e-3 if B * N >= 4096 else None)
+
+
 def test_force_safe_env_routes_to_fp32_kernel(monkeypatch):
     x, c = _data(1, 2048, 128, 128, "f16", seed=21)
     monkeypatch.setenv("FKC_ASSIGN_FORCE_SAFE", "1")
