@@ -56,6 +56,7 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <atomic>
 #include <math.h>
 
 namespace fkc {
@@ -1028,14 +1029,22 @@ int launch_resident_t(const void* x, const void* c, const float* c_sq,
                       int32_t* ids, int64_t B, int64_t N, int64_t K,
                       const int32_t* ctrl, hipStream_t s, hipEvent_t ev0,
                       hipEvent_t ev1) {
-  // Dynamic LDS above the default limit needs the kernel's attribute raised
-  // once per process.
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&assign_resident_kernel<DT, DS2, PT, W>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kResidentLds);
-  if (attr != hipSuccess)
-    return fail(FKC_ERR_LAUNCH, "assign_resident: LDS attribute: %s",
-                hipGetErrorString(attr));
+  // Dynamic LDS above the default limit needs the kernel's attribute raised,
+  // once per device (a bit per device id; the call is not a stream
+  // operation, so it is also allowed while the stream is being captured).
+  static std::atomic<uint64_t> raised{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(FKC_ERR_LAUNCH, "assign_resident: no current device");
+  if (!(raised.load(std::memory_order_acquire) & (1ull << dev))) {
+    const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&assign_resident_kernel<DT, DS2, PT, W>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, kResidentLds);
+    if (attr != hipSuccess)
+      return fail(FKC_ERR_LAUNCH, "assign_resident: LDS attribute: %s",
+                  hipGetErrorString(attr));
+    raised.fetch_or(1ull << dev, std::memory_order_acq_rel);
+  }
   const int Kp = (int)((K + 31) & ~31);
   const size_t lds = (size_t)resident_bytes(DS2, Kp);
   dim3 grid((unsigned)resident_grid(PT, W, B, N), (unsigned)B);

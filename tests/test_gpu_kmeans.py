@@ -532,6 +532,64 @@ def test_lloyd_iteration_captures_into_a_graph():
         state = e_c
 
 
+_FIRST_CALL_CAPTURED = r'''
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from flash_kmeans_cuda import _lib
+L = _lib.lib
+B, N, K, D = 2, 8192, 700, 64
+g = torch.Generator(device="cuda").manual_seed(0)
+x = torch.randn(B, N, D, device="cuda", generator=g).to(torch.bfloat16)
+cents = x[:, :K].contiguous().clone()
+ids = torch.empty((B, N), dtype=torch.int32, device="cuda")
+dt = _lib.dtype_code(x.dtype)
+ws = _lib.workspace(L.fkc_kmeans_workspace_bytes(B, N, K, D, dt, 1), x.device)
+s = torch.cuda.Stream()
+
+
+def one():
+    _lib.check(L.fkc_kmeans_lloyd(x.data_ptr(), cents.data_ptr(), ids.data_ptr(), B, N, K,
+                                  D, dt, 1, 0.0, ws.data_ptr(), ws.numel(), s.cuda_stream,
+                                  None, None), "kmeans_lloyd")
+
+
+start = cents.clone()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=s):
+    one()
+torch.cuda.synchronize()
+for rep in range(3):
+    cents.copy_(start)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        one()
+    torch.cuda.synchronize()
+    e_c, e_i = cents.clone(), ids.clone()
+    cents.copy_(start)
+    ids.fill_(-1)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(cents, e_c) and torch.equal(ids, e_i), f"replay {rep}"
+print("graph-ok", flush=True)
+'''
+
+
+def test_resident_assign_first_launched_inside_graph_capture():
+    """A process whose first centroid-resident launch is inside HIP graph
+    capture (the launcher raises the kernel's LDS attribute on a device's
+    first use): every replay of the captured Lloyd iteration equals the
+    eager one.  A fresh interpreter, so no earlier call raised it."""
+    import subprocess
+    import sys
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                       "flash-kmeans-cuda_amd")
+    env = dict(os.environ, FKC_RESIDENT="1")
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, pkg], env=env,
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "graph-ok" in r.stdout, (r.stdout[-2000:], r.stderr[-2000:])
+
+
 def test_two_threads_on_two_streams_with_profiling():
     """The entry points keep no state across calls beyond the profiling
     hook: two host threads run the Lloyd loop at once, each on its own
