@@ -78,6 +78,13 @@ int resident_override() {
   return std::strcmp(s, "1") == 0 ? 1 : (std::strcmp(s, "0") == 0 ? 0 : -1);
 }
 
+int update_rows_override() {
+  const char* s = std::getenv("FKC_UPDATE_ROWS");
+  if (!s) return 0;
+  const int v = std::atoi(s);
+  return (v == 32 || v == 64 || v == 128) ? v : 0;
+}
+
 bool sort_fuse_override() {
   const char* s = std::getenv("FKC_SORT_FUSE");
   return !(s && std::strcmp(s, "0") == 0);

@@ -197,5 +197,8 @@ int save_override();
 // FKC_RESIDENT=0|1: centroid-resident assign off / on where the table fits
 // in LDS; -1 = auto.
 int resident_override();
+// FKC_UPDATE_ROWS=32|64|128: sorted rows per unit of the centroid update;
+// 0 = auto.
+int update_rows_override();
 
 }  // namespace fkc

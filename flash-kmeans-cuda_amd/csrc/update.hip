@@ -59,10 +59,10 @@ constexpr int UR_MAX = 128;  // sorted rows per unit (one wave), at most
 
 // Rows per unit: 128 when that still gives >= 2048 units (512 workgroups),
 // else 64, else 32 — small N needs the extra waves to hide its latency.
+// FKC_UPDATE_ROWS=32|64|128 overrides (A/B runs; the workspace query and
+// the launch read it alike).
 int choose_ur(int64_t B, int64_t N) {
-#ifdef FKC_UR_FORCE
-  return FKC_UR_FORCE;
-#endif
+  if (const int o = update_rows_override()) return o;
   for (int ur = UR_MAX; ur > 32; ur >>= 1)
     if (B * ((N + ur - 1) / ur) >= 2048) return ur;
   return 32;
