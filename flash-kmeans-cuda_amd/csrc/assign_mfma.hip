@@ -79,7 +79,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // FKC_KC_DMA, centroid rows per direct stage at D = 97..128 (x4 at D = 32,
 // x2 at D = 64); FKC_KC_DMA8, the
 // same for the eight-tile variant (two workgroups per CU leave it twice the
-// LDS); FKC_SLICE_MIN_ROWS, the shortest centroid slice; FKC_SCHED_GROUPS,
+// LDS; at c5, bench defaults, same box: 128 rows 0.795 / 0.797 ms per
+// iteration, 144 rows 0.798 / 0.799 (four registers spilled), 96 rows
+// 0.799 / 0.801); FKC_SLICE_MIN_ROWS, the shortest centroid slice; FKC_SCHED_GROUPS,
 // LDS-read / MFMA / VALU ordering hints in the direct-stage loop.
 #ifndef FKC_AB
 #define FKC_AB 2
