@@ -13,6 +13,11 @@ the configuration's own max_iters and tol.  <config>_full.npz holds:
   n_iters     iterations run (c4 stops after the first shift below tol)
   shifts      float32 [iters]: the shift of every iteration (kmeans.py:104)
   labels      uint16 (B, N): labels of the last assignment (kmeans.py:179-195)
+  assigned_against
+              (B, K, D) raw storage bits of the centroids that last
+              assignment ranked (the state after n_iters - 1 iterations, or
+              the initial centroids when n_iters = 1), so a test can assign
+              every point against exactly them
   centroids   (B, K, D) final centroids, raw storage bits (uint16)
   inertia     float64: sum over every point of the exact squared distance to
               its nearest final centroid (the objective the bar compares)
@@ -91,6 +96,7 @@ def make(name: str) -> str:
         n_iters=np.array(n),
         shifts=np.array(shifts, dtype=np.float32),
         labels=traj_ids[n - 1].astype(np.uint16),
+        assigned_against=_bits(traj_c[n - 2] if n >= 2 else init),
         centroids=_bits(traj_c[n - 1]),
         inertia=np.array(_nearest_inertia(x, traj_c[n - 1], cfg.dtype)),
     )

@@ -108,3 +108,58 @@ def test_c5_full_size_assignment_is_exact_up_to_near_ties():
                                      ids10.cpu().numpy()[:, sub], ref)
     print(f"c5 iteration 10 on 8192 sampled points: {nd} near-tie flips, worst gap {worst:.2e}")
     assert bad == 0 and nd / sub.size < 1e-3
+
+
+def test_c5_every_point_against_the_oracle_step():
+    """c5's 10th iteration, one step at a time, on all 524288 points, against
+    the oracle's own state (tests/golden/c5_full.npz): the GPU assigns every
+    point against the centroids the oracle's 10th assignment ranked
+    (assigned_against) and its labels equal the oracle's except on near-ties
+    (< 0.1% of points, none with an exact-distance gap above the fp32 bound);
+    the GPU's label sort of its own labels equals the oracle's stable sort bit
+    for bit (sorted labels and permutation); the update's counts are exact and
+    its fp32 sums within fp32 accumulation error of the oracle's float64 sums;
+    the finalize of the GPU's sums equals the oracle's finalize of the same
+    sums bit for bit (kmeans.py:179-195; quality_compare.py:110-114 measures
+    label disagreement over every point the same way)."""
+    from flash_kmeans_cuda import _C, ops, synth
+    cfg = synth.CONFIGS["c5"]
+    z = np.load(os.path.join(GOLDEN, "c5_full.npz"))
+    assert "assigned_against" in z.files, "fixture predates assigned_against"
+    x, _ = synth.make(cfg)
+    assert hashlib.sha256(x.tobytes()).hexdigest() == str(z["x_sha256"]), "inputs differ"
+    c9 = _storage(z["assigned_against"], cfg.dtype)
+    want = z["labels"].astype(np.int64)
+    xt, ct = synth.to_torch(x, cfg.dtype), synth.to_torch(c9, cfg.dtype)
+
+    # assign: every point
+    ids_t = _C.euclid_assign(xt, ct, ops.row_sqnorm(xt), ops.row_sqnorm(ct))
+    ids = ids_t.cpu().numpy().astype(np.int64)
+    nd, bad, worst = near_tie_report(x, c9, cfg.dtype, ids, want)
+    print(f"c5 assign vs oracle on all {cfg.N} points: {nd} differ "
+          f"({nd / cfg.N:.5%}), {bad} beyond the near-tie bound, worst gap {worst:.2e}")
+    assert bad == 0 and nd / ids.size < 1e-3
+
+    # sort of the GPU labels: bit-exact against the stable sort
+    s_t, p_t = ops.label_sort(ids_t, cfg.K)
+    e_s, e_p = O.label_sort(ids, cfg.K)
+    assert np.array_equal(s_t.cpu().numpy(), e_s) and np.array_equal(p_t.cpu().numpy(), e_p)
+
+    # update through the permutation: exact counts, fp32-close sums
+    sums = torch.zeros((1, cfg.K, cfg.D), device="cuda")
+    cnt = torch.zeros((1, cfg.K), device="cuda", dtype=torch.int32)
+    _C.centroid_update_sorted_indexed(xt, p_t, s_t, sums, cnt)
+    es, ec = O.update_sorted_indexed(x, e_p, e_s, cfg.K, cfg.dtype)
+    g_s, g_c = sums.cpu().numpy(), cnt.cpu().numpy()
+    assert np.array_equal(g_c, ec) and int(ec.sum()) == cfg.N
+    # fp32 accumulation of n rows: within 1e-6 * n * max|x| plus 1e-6 relative
+    tol = (1e-6 * np.maximum(ec[..., None], 1) * np.abs(O.to_f64(x, cfg.dtype)).max()
+           + 1e-6 * np.abs(es))
+    assert np.all(np.abs(g_s - es) <= tol), float(np.abs(g_s - es).max())
+    assert np.all(g_s[ec == 0] == 0)
+
+    # finalize of the GPU's own sums: bit-exact
+    new_t = _C.centroid_finalize(sums, cnt, ct)
+    exp = O.finalize(g_s, g_c, c9, cfg.dtype)
+    got = synth.from_torch(new_t, cfg.dtype)
+    assert np.array_equal(np.asarray(got).view(np.uint16), np.asarray(exp).view(np.uint16))

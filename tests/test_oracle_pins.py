@@ -342,6 +342,94 @@ def test_row_sqnorm_pinned():
             assert got[i, j] == pytest.approx(math.fsum(float(t) ** 2 for t in v[i, j]), rel=1e-15)
 
 
+# ================================================================= distances
+def _distances_battery(dist_fn):
+    """dist_fn(x, c, dtype, ids) -> float64 (B, N): the exact squared distance
+    of every point to its labelled centroid (the figure the frozen fixtures'
+    inertia and the GPU tests' inertia checks are summed from)."""
+    import math
+    fails = []
+    rng = _rng(9)
+    # 1. brute force (exact sums of Python floats) for every storage dtype,
+    # batch rows with their own tables and labels
+    for dtype in ("f32", "f16", "bf16", "f64"):
+        B, N, K, D = 3, 19, 5, 7
+        xf = (rng.standard_normal((B, N, D)) * 3).astype(np.float32)
+        cf = (rng.standard_normal((B, K, D)) * 3).astype(np.float32)
+        x = O.from_f32(xf, dtype) if dtype != "f64" else xf.astype(np.float64)
+        c = O.from_f32(cf, dtype) if dtype != "f64" else cf.astype(np.float64)
+        ids = rng.integers(0, K, (B, N)).astype(np.int32)
+        got = dist_fn(x, c, dtype, ids)
+        if got.shape != (B, N):
+            fails.append(f"shape {got.shape}")
+            continue
+        xv, cv = O.to_f64(x, dtype), O.to_f64(c, dtype)
+        for b in range(B):
+            for n in range(N):
+                want = math.fsum((float(p) - float(q)) ** 2
+                                 for p, q in zip(xv[b, n], cv[b, ids[b, n]]))
+                if not math.isclose(float(got[b, n]), want, rel_tol=1e-14, abs_tol=1e-300):
+                    fails.append(f"brute {dtype} ({b},{n}): {got[b, n]!r} vs {want!r}")
+                    break
+    # 2. library: scipy's vq returns the Euclidean distance to the nearest
+    # centroid; its square at vq's labels is this function at those labels
+    from scipy.cluster.vq import vq
+    x = rng.standard_normal((1, 400, 12))
+    c = rng.standard_normal((1, 30, 12))
+    lab, dist = vq(x[0], c[0])
+    got = dist_fn(x, c, "f64", lab[None].astype(np.int64))
+    if not np.allclose(got[0], dist ** 2, rtol=1e-12, atol=0):
+        fails.append("scipy vq distances")
+    # 3. known answers: a 3-4-5 triangle and a point on its own centroid
+    c = np.zeros((1, 2, 3), np.float32)
+    c[0, 1] = (1.0, 1.0, 1.0)
+    x = np.array([[[3.0, 4.0, 0.0], [1.0, 1.0, 1.0]]], np.float32)
+    got = dist_fn(x, c, "f32", np.array([[0, 1]], np.int32))
+    if list(map(float, got[0])) != [25.0, 0.0]:
+        fails.append(f"known answers {got[0]}")
+    return fails
+
+
+def _mut_dist_not_squared(x, c, dtype, ids):
+    return np.sqrt(O.distances(x, c, dtype, ids))
+
+
+def _mut_dist_first_row_table(x, c, dtype, ids):
+    # every batch row scored against batch row 0's centroids
+    c0 = np.broadcast_to(np.asarray(c)[:1], np.asarray(c).shape).copy()
+    return O.distances(x, c0, dtype, ids)
+
+
+def _mut_dist_label_off_by_one(x, c, dtype, ids):
+    K = np.asarray(c).shape[1]
+    return O.distances(x, c, dtype, (np.asarray(ids) + 1) % K)
+
+
+def _mut_dist_f16_values(x, c, dtype, ids):
+    # distances computed from values rounded to fp16 (a precision mistake)
+    xv = O.to_f64(x, dtype).astype(np.float16).astype(np.float64)
+    cv = O.to_f64(c, dtype).astype(np.float16).astype(np.float64)
+    chosen = np.take_along_axis(cv, np.asarray(ids).astype(np.int64)[..., None], axis=1)
+    return ((xv - chosen) ** 2).sum(-1)
+
+
+def _mut_dist_dropped_feature(x, c, dtype, ids):
+    xv, cv = O.to_f64(x, dtype), O.to_f64(c, dtype)
+    chosen = np.take_along_axis(cv, np.asarray(ids).astype(np.int64)[..., None], axis=1)
+    return ((xv - chosen)[..., 1:] ** 2).sum(-1)
+
+
+def test_distances_oracle_pinned():
+    assert _distances_battery(O.distances) == []
+
+
+@pytest.mark.parametrize("mutant", [_mut_dist_not_squared, _mut_dist_first_row_table,
+                                    _mut_dist_label_off_by_one, _mut_dist_f16_values,
+                                    _mut_dist_dropped_feature])
+def test_distances_battery_rejects_planted_mistakes(mutant):
+    assert _distances_battery(mutant) != []
+
+
 # ====================================================================== loop
 def _loop_battery(kmeans_fn):
     fails = []
