@@ -18,14 +18,16 @@ Reported:
                         run of 5 in the timed region (iterations 2, 7, 12,
                         ...), on the launch stream
   roofline              assign kernel against the fp16 dense MFMA peak
-  cpu_baseline          the CPU oracle (numpy fp32 BLAS restatement of the
-                        same loop) on a bounded sample, scaled to full N
+  cpu_baseline          the torch-CPU restatement of the same loop
+                        (oracle/torch_cpu.py) on the full data: 1 warm-up,
+                        median of 3 runs, as ms/iter
   ms_per_iter_ref_method  one whole call with max_iters=1 (README.md:221 of
                         the reference)
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--config c5]
-       python bench.py --report        per-config table (c1..c5, c5s8 = c5 on one of 8
-                                       N-shards): assign TFLOPS,
+       python bench.py --report        per-config table (c1..c5, huge = the
+                                       reference's (1, 262144, 4096, 128) shape,
+                                       c5s8 = c5 on one of 8 N-shards): assign TFLOPS,
                                        ms/iter (steady state and one-iteration
                                        call), roofline fraction ideal/measured
        python bench.py --assign-sweep  euclid_assign alone over a list of shapes
@@ -52,8 +54,10 @@ PEAK_TFLOPS_F32 = 157.3           # MI355X fp32 (the fp32 route runs on the VALU
 METRIC_C5 = "assign TFLOPS + end-to-end ms/iter at (1,524K,8192,128) fp16, 1 MI355X"
 PROFILE_PERIOD = 5                # event-time the assign of one timed iteration in 5
 PEAK_HBM_GBS = 8000.0
-REF_MS_PER_ITER = {"c5": 6.179, "c3": 0.489, "c2": 0.129}   # README.md:31-34 (RTX 4090)
-REF_ASSIGN_TFLOPS = {"c5": 185.0, "c3": 171.0, "c2": 92.0}  # README.md:21-24
+# README.md:31-34 and 21-24 of the reference (RTX 4090, fp16, D = 128): its
+# med / big / huge / mega shapes are c2 / c3 / huge / c5 here
+REF_MS_PER_ITER = {"c5": 6.179, "huge": 1.667, "c3": 0.489, "c2": 0.129}
+REF_ASSIGN_TFLOPS = {"c5": 185.0, "huge": 176.0, "c3": 171.0, "c2": 92.0}
 
 
 def _traffic_from_profiles(cfg_name: str):
@@ -67,35 +71,73 @@ def _traffic_from_profiles(cfg_name: str):
         return None
 
 
-def _cpu_baseline(cfg, x_np, init_np, sample_n: int, iters: int):
-    """`iters` Lloyd iterations of the oracle on the first sample_n points
-    (0: all N; full K, D), fp32 BLAS assign; ms/iter, scaled linearly to the
-    full N when sampled.  The defaults (all of c5, 2 iterations) are about
-    10 s of CPU work on the GPU box's 16 threads."""
-    import numpy as np
-    from oracle import kmeans_oracle as O
-    sample_n = cfg.N if sample_n <= 0 else min(sample_n, cfg.N)
-    iters = max(iters, 1)
-    xs = np.ascontiguousarray(x_np[:, :sample_n])
+CPU_BUDGET_S = 30.0  # timed CPU work of the baseline (3 runs), about
+
+
+def _cpu_baseline(cfg, x_np, init_np, iters=None, budget_s=CPU_BUDGET_S):
+    """The torch-CPU restatement of the Lloyd loop (oracle/torch_cpu.py) on
+    the configuration's full data (every point, full K and D), timed with
+    time.perf_counter: one warm-up run of one iteration, then the median of
+    3 timed runs of `iters` iterations each, as ms/iter.  `iters` defaults to
+    the configuration's max_iters when 3 such runs fit `budget_s` (judged
+    from the warm-up), else to as many as fit (c5: a few of its 10; the
+    sample string says which).  Runs use tol = 0 so every one does the same
+    work; cores = torch's intra-op threads."""
+    import statistics
+    import torch
+    from flash_kmeans_cuda import synth
+    from oracle import torch_cpu
+    x = synth.to_torch(x_np, cfg.dtype, device="cpu")
+    init = synth.to_torch(init_np, cfg.dtype, device="cpu")
     t0 = time.perf_counter()
-    O.kmeans(xs, cfg.K, iters, 0.0, init_np, cfg.dtype, precision="f32")
-    dt = (time.perf_counter() - t0) / iters
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        cores = os.cpu_count() or 1
+    torch_cpu.kmeans(x, init, 1, 0.0)
+    t_one = time.perf_counter() - t0
+    if iters is None:
+        fit = int(budget_s // (3 * max(t_one, 1e-9)))
+        iters = cfg.iters if fit >= cfg.iters else max(1, fit)
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch_cpu.kmeans(x, init, iters, 0.0)
+        runs.append(time.perf_counter() - t0)
+    med = statistics.median(runs)
+    threads = torch.get_num_threads()
     return {
-        "value": dt * 1e3 * (cfg.N / sample_n),
+        "value": med * 1e3 / iters,
         "unit": "ms/iter",
-        "cores": int(cores),
+        "cores": int(threads),
         "kind": "port",
-        "sample": (f"{iters} Lloyd iterations of the numpy oracle (fp32 BLAS assign, stable "
-                   f"sort, float64 sums) on " + (f"all {cfg.N}" if sample_n == cfg.N else
-                                                f"the first {sample_n} of {cfg.N}") +
-                   f" points, K={cfg.K}, D={cfg.D}; {dt * iters:.1f} s measured"
-                   + ("" if sample_n == cfg.N else f", scaled x{cfg.N / sample_n:g} to full N")),
+        "sample": (f"torch-CPU restatement of the loop (fp32 matmul assign, stable torch.sort, "
+                   f"fp32 index_add sums, fp32 finalize) on all {cfg.B}x{cfg.N} points, "
+                   f"K={cfg.K}, D={cfg.D} {cfg.dtype}: 1 warm-up run of 1 iteration, median of "
+                   f"3 runs of {iters} iteration(s)"
+                   + ("" if iters == cfg.iters else
+                      f" (max_iters is {cfg.iters}; {iters} per run keeps the 3 runs within "
+                      f"~{budget_s:.0f} s)")
+                   + f"; runs {', '.join(f'{r:.2f}' for r in runs)} s; "
+                   f"torch threads {threads}, os.cpu_count() {os.cpu_count()}"),
     }
+
+
+def _sort_recounts(x, init, cfg, iters: int) -> int:
+    """One Lloyd call of `iters` iterations through the C ABI with a
+    workspace of our own, then the label sort's recount word of that call
+    (fkc_kmeans_sort_recounts_offset): tiles whose bounded wait ran out."""
+    import torch
+    from flash_kmeans_cuda import _lib
+    dt = _lib.dtype_code(x.dtype)
+    L = _lib.lib
+    ws = _lib.workspace(L.fkc_kmeans_workspace_bytes(cfg.B, cfg.N, cfg.K, cfg.D, dt, iters),
+                        x.device)
+    cents = torch.empty_like(init)
+    ids = torch.empty((cfg.B, cfg.N), dtype=torch.int32, device=x.device)
+    _lib.check(L.fkc_kmeans_lloyd_from(
+        x.data_ptr(), init.data_ptr(), cents.data_ptr(), ids.data_ptr(), cfg.B, cfg.N,
+        cfg.K, cfg.D, dt, iters, 0.0, ws.data_ptr(), ws.numel(), _lib.stream_of(x),
+        None, None), "kmeans_lloyd_from")
+    off = L.fkc_kmeans_sort_recounts_offset(cfg.B, cfg.N, cfg.K, cfg.D, dt, iters)
+    torch.cuda.synchronize()
+    return int(ws[off:off + 4].view(torch.int32).item())
 
 
 COPY_FLOATS = 64 << 20  # calibration kernel: reads and writes 256 MiB
@@ -255,9 +297,8 @@ def _report(configs) -> int:
     loop's steady state (one call of cfg.iters iterations, tol = 0, per
     iteration, best of 5 calls), the
     reference's methodology (one whole call with max_iters=1, best of 5), the
-    roofline fraction ideal / measured per iteration, and the CPU oracle's
-    ms/iter on the same inputs (2 iterations on every point, BLAS threads
-    stated)."""
+    roofline fraction ideal / measured per iteration, and the torch-CPU
+    restatement's ms/iter on the same inputs (threads stated)."""
     import statistics
     import torch
     from flash_kmeans_cuda import _C, batch_kmeans_Euclid, synth
@@ -303,9 +344,9 @@ def _report(configs) -> int:
             torch.cuda.synchronize()
             one.append((time.perf_counter() - t0) * 1e3)
         flops, byts, ideal = _ideal_ms(cfg)
-        # The CPU oracle on the same inputs: 2 iterations on every point
-        # (the loop's fp32 BLAS form), a few seconds per config at most.
-        cpu = _cpu_baseline(cfg, x_np, init_np, 0, 2)
+        # The torch-CPU restatement on the same inputs (every point), its
+        # runs kept within ~15 s per config.
+        cpu = _cpu_baseline(cfg, x_np, init_np, budget_s=15.0)
         row = {
             "config": name, "B": cfg.B, "N": cfg.N, "K": cfg.K, "D": cfg.D,
             "dtype": cfg.dtype, "assign_ms": round(assign_ms, 5),
@@ -344,10 +385,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="c5")
-    ap.add_argument("--cpu-sample", type=int, default=0,
-                    help="points of the CPU baseline sample (0: all N)")
-    ap.add_argument("--cpu-iters", type=int, default=2,
-                    help="Lloyd iterations of the CPU baseline")
+    ap.add_argument("--cpu-iters", type=int, default=None,
+                    help="Lloyd iterations per timed run of the CPU baseline (default: "
+                         "the config's max_iters, or fewer to keep its runs within ~30 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one elementwise copy kernel of "
@@ -360,7 +400,7 @@ def main() -> int:
                          "(torch.matmul) on large fp16 / bf16 shapes")
     ap.add_argument("--assign-sweep", action="store_true",
                     help="euclid_assign alone over a fixed list of shapes (ms, TFLOP/s)")
-    ap.add_argument("--report", nargs="?", const="c1,c2,c3,c4,c5,c5s8", default=None,
+    ap.add_argument("--report", nargs="?", const="c1,c2,c3,huge,c4,c5,c5s8", default=None,
                     help="per-configuration table (comma-separated config names)")
     args = ap.parse_args()
 
@@ -430,6 +470,10 @@ def main() -> int:
         torch.cuda.synchronize()
         one.append((time.perf_counter() - s) * 1e3)
 
+    # the sort's recount word after a loop call of the same shape (0 when its
+    # grid ran at once, as it should on an otherwise idle GPU)
+    recounts = _sort_recounts(x, init, cfg, args.steps)
+
     # quick parity sample: labels of 2048 points vs the exact oracle
     from oracle import kmeans_oracle as O
     c_np = synth.from_torch(cents, cfg.dtype)
@@ -481,10 +525,10 @@ def main() -> int:
             "traffic": traffic,
         },
         "parity_sample": {"points": int(sub.size), "label_disagreements": disagree},
+        "sort_recounts": recounts,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = _cpu_baseline(cfg, x_np, init_np, args.cpu_sample,
-                                             args.cpu_iters)
+        line["cpu_baseline"] = _cpu_baseline(cfg, x_np, init_np, args.cpu_iters)
     print(json.dumps(line), flush=True)
     return 0
 

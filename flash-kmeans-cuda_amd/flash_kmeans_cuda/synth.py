@@ -49,6 +49,10 @@ CONFIGS = {
                  "mixture", seed=0, init_seed=100, per_batch_seed=True),
     "c5": Config("c5_f16_k8192_zipf", 1, 524288, 8192, 128, "f16", 10, 0.0,
                  "mixture", zipf=1.1),
+    # The reference's fourth published shape ("huge", README.md:23,33 of the
+    # reference: 176 TFLOP/s assign, 1.667 ms/iter on an RTX 4090), not a
+    # BASELINE config: a uniform mixture of 4096 blobs like c3.
+    "huge": Config("huge_f16_k4096", 1, 262144, 4096, 128, "f16", 10, 0.0, "mixture"),
     # One GPU's share when c5 is sharded over N on 8 GPUs (65536 points, all
     # 8192 centroids): the per-rank assign, sort and update at their real
     # shape, without the per-iteration all-reduce of sums and counts.
