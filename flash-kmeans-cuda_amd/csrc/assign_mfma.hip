@@ -110,6 +110,17 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #ifndef FKC_SCHED_GROUPS
 #define FKC_SCHED_GROUPS 1
 #endif
+// FKC_X_NT=1: point rows are loaded with the non-temporal hint.  Each point
+// row is read by one workgroup, once, so the assign itself gains nothing
+// from caching it, and without the hint the streaming rows evict centroid
+// stages from L2 (c5: 186 MB fetched per launch against 138 MB of
+// algorithmic bytes; with the hint 154 MB, same assign time).  Off by
+// default: the Lloyd iteration then ran 6-7 us slower at c5 (0.797 against
+// 0.790 ms, same box, alternating runs), the update's gathers of the same
+// rows finding fewer of them in the device's last-level cache.
+#ifndef FKC_X_NT
+#define FKC_X_NT 0
+#endif
 
 constexpr int KC = 64;  // centroid rows per register-staged LDS stage
 constexpr int THREADS = 256;  // 4 waves
@@ -136,6 +147,15 @@ __device__ inline f32x4 mfma16<FKC_BF16>(u32x4 a, u32x4 b, f32x4 c) {
 template <int SEGS>
 __device__ constexpr int swz(int r) {
   return SEGS >= 16 ? (r & 15) : ((r & 15) / (16 / SEGS));
+}
+
+// One 16-byte piece of a point row (see FKC_X_NT).
+__device__ inline u32x4 load_point(const u32x4* p) {
+#if FKC_X_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
 }
 
 // Running maximum of a lane's scores.  The main loop keeps, per lane and
@@ -264,7 +284,8 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
 #pragma unroll
     for (int s = 0; s < DS2; ++s) {
       const int seg = 4 * s + g;
-      xr[p][s] = (!padded || seg < dsegs) ? src[seg] : u32x4{0u, 0u, 0u, 0u};
+      xr[p][s] = (!padded || seg < dsegs) ? load_point(src + seg)
+                                          : u32x4{0u, 0u, 0u, 0u};
     }
   }
 
@@ -769,8 +790,9 @@ assign_merge_kernel(const float* __restrict__ psc,
 // ------------------------------------------------------------------------
 // Centroid-resident variant.  When a batch row's whole centroid table fits
 // in one workgroup's LDS (Kp = K rounded up to 32 rows of DP features, plus
-// Kp scaled c_sq values: resident_bytes(Kp) <= kResidentLds, i.e. K <= 1216
-// at D = 64 and K <= 2400 at D = 32), each workgroup loads the table once
+// Kp scaled c_sq values: resident_bytes(Kp) <= the device's LDS per
+// workgroup, i.e. on gfx950's 160 KiB K <= 1216 at D = 64 and K <= 2400 at
+// D = 32), each workgroup loads the table once
 // and its waves then walk their 16*PT-point tiles against it on their own:
 // no stage loads or barriers in the loop, the winner's candidate rows are
 // scored again from LDS rather than L2, and a wave that is loading its next
@@ -778,8 +800,8 @@ assign_merge_kernel(const float* __restrict__ psc,
 // of its SIMD instead of idling it for a whole round of workgroups.  The
 // scores are the same MFMA chains with the same seeds as the staged kernel,
 // folded by the same block rule and re-score, so the labels are identical.
-constexpr int kCUs = 256;                 // MI355X compute units
-constexpr int kResidentLds = 160 * 1024;  // LDS one workgroup may hold (gfx950)
+// The table's LDS bound is the device's per-workgroup LDS (160 KiB on
+// gfx950, read with the CU count by device_shape()).
 constexpr int kResidentWaves = 16;        // waves per workgroup (4 per SIMD)
 
 __host__ __device__ constexpr int resident_bytes(int ds2, int Kp) {
@@ -1022,7 +1044,7 @@ static int64_t resident_need(int pt, int w, int64_t N) {
 }
 
 static int resident_grid(int pt, int w, int64_t B, int64_t N) {
-  const int64_t fill = std::max<int64_t>(1, kCUs / B);
+  const int64_t fill = std::max<int64_t>(1, device_shape().cus / B);
   return (int)std::max<int64_t>(1, std::min(resident_need(pt, w, N), fill));
 }
 
@@ -1041,7 +1063,8 @@ int launch_resident_t(const void* x, const void* c, const float* c_sq,
   if (!(raised.load(std::memory_order_acquire) & (1ull << dev))) {
     const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&assign_resident_kernel<DT, DS2, PT, W>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, kResidentLds);
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        device_shape().lds_per_wg);
     if (attr != hipSuccess)
       return fail(FKC_ERR_LAUNCH, "assign_resident: LDS attribute: %s",
                   hipGetErrorString(attr));
@@ -1186,14 +1209,16 @@ bool assign_uses_mfma(int dtype, int64_t D) {
          D <= 512 && !force_safe_assign();
 }
 
-// Workgroups an unsliced launch of pt tiles needs to fill the chip: 1024
-// (4 per CU) in general; 256 (one per CU, one wave per SIMD) suffice for
-// four tiles at D = 97..128, whose 16 MFMAs per centroid block keep a lone
-// wave busy (measured at N = 131072, K = 2048 and N = 65536, K = 8192:
-// four tiles on 512 / 256 workgroups beat two tiles on 1024 / 512 by 3% /
-// 5%); eight tiles run 2 workgroups per CU and need two rounds of them.
+// Workgroups an unsliced launch of pt tiles needs to fill the chip: 4 per
+// CU in general; one per CU (one wave per SIMD) suffices for four tiles at
+// D = 97..128, whose 16 MFMAs per centroid block keep a lone wave busy
+// (measured on MI355X's 256 CUs at N = 131072, K = 2048 and N = 65536,
+// K = 8192: four tiles on 512 / 256 workgroups beat two tiles on 1024 / 512
+// by 3% / 5%); eight tiles run 2 workgroups per CU and need two rounds of
+// them.
 static int64_t fill_wgs(int pt, int ds2, bool exact) {
-  return (!exact && pt == 4 && ds2 == 4) ? 256 : 1024;
+  const int64_t cus = device_shape().cus;
+  return (!exact && pt == 4 && ds2 == 4) ? cus : 4 * cus;
 }
 
 static int64_t grid_wgs(int pt, int64_t B, int64_t N) {
@@ -1258,12 +1283,13 @@ static int resident_pt(int ds2) { return ds2 == 1 ? 8 : 4; }
 static bool use_resident(const Plan& p, int64_t B, int64_t N, int64_t K) {
   if (p.pad || (p.ds2 != 1 && p.ds2 != 2)) return false;
   const int64_t Kp = (K + 31) & ~int64_t{31};
-  if (Kp * (p.ds2 * 64 + 4) > kResidentLds) return false;
+  const DeviceShape dev = device_shape();
+  if (Kp * (p.ds2 * 64 + 4) > dev.lds_per_wg) return false;
   const int o = resident_override();
   if (o >= 0) return o == 1;
   const int pt = resident_pt(p.ds2);
   return K > FKC_EXACT_MAX_K_NARROW &&
-         B * resident_need(pt, kResidentWaves, N) >= kCUs;
+         B * resident_need(pt, kResidentWaves, N) >= dev.cus;
 }
 
 // Launch plan.  K is sliced only when no unsliced grid fills the chip (few
@@ -1313,11 +1339,12 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   int64_t S = ksplit_override();
   if (S == 0 && pt == 4 && p.ds2 == 4) {
     // D = 97..128: as many slices as fit one round of the 167-VGPR
-    // variant's 768 resident workgroups (3 per CU).  One round, not two: at
-    // N = 65536, K = 8192 three slices took 0.117 ms, four 0.122, none
-    // 0.121; at N = 32768, K = 16384 six 0.123, three 0.138, none 0.220;
-    // at N = 131072, K = 4096 two slices (two rounds) lost 6%.
-    S = std::min<int64_t>(768 / tiles, K / FKC_SLICE_MIN_ROWS);
+    // variant's resident workgroups (3 per CU, 768 on MI355X).  One round,
+    // not two: at N = 65536, K = 8192 three slices took 0.117 ms, four
+    // 0.122, none 0.121; at N = 32768, K = 16384 six 0.123, three 0.138,
+    // none 0.220; at N = 131072, K = 4096 two slices (two rounds) lost 6%.
+    S = std::min<int64_t>(3 * device_shape().cus / tiles,
+                          K / FKC_SLICE_MIN_ROWS);
     if (S <= 1) return p;
   } else if (S == 0) {
     const int64_t want = fill_wgs(pt, p.ds2, p.exact);

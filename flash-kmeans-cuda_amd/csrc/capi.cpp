@@ -98,6 +98,59 @@ int sort_spin_override(int dflt) {
   return (*end == 0 && v >= 0 && v <= dflt) ? (int)v : dflt;
 }
 
+// Device shape, read once per device (the attributes cannot change while
+// the process runs); without a usable device (a CPU host asking for
+// workspace sizes) the MI355X figures stand in.
+DeviceShape device_shape() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> g_cus[kMaxDev];  // 0: not read yet
+  static std::atomic<int> g_lds[kMaxDev];
+  static std::atomic<bool> g_nodev{false};  // no device: asked once
+  DeviceShape d{kMi355xCUs, kMi355xLds};
+  int dev = -1;
+  if (g_nodev.load(std::memory_order_relaxed)) {
+  } else if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();  // no device here: do not leave a sticky error
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+      g_nodev.store(true, std::memory_order_relaxed);
+    (void)hipGetLastError();
+  } else {
+    int cus = g_cus[dev].load(std::memory_order_acquire);
+    int lds = g_lds[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+      int c = 0, l = 0;
+      if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount,
+                                dev) != hipSuccess)
+        c = 0;
+      // LDS one workgroup may use once its kernel opts in (160 KiB on
+      // gfx950), else the LDS of a CU.
+      if (hipDeviceGetAttribute(&l, hipDeviceAttributeSharedMemPerBlockOptin,
+                                dev) != hipSuccess ||
+          l <= 0) {
+        if (hipDeviceGetAttribute(
+                &l, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) !=
+            hipSuccess)
+          l = 0;
+      }
+      (void)hipGetLastError();
+      cus = c > 0 ? c : kMi355xCUs;
+      lds = l > 0 ? l : kMi355xLds;
+      g_lds[dev].store(lds, std::memory_order_relaxed);
+      g_cus[dev].store(cus, std::memory_order_release);
+    }
+    d.cus = cus;
+    d.lds_per_wg = lds;
+  }
+  // FKC_CUS=n (tests, A/B runs): plan as if the device had n compute units.
+  if (const char* s = std::getenv("FKC_CUS")) {
+    char* end = nullptr;
+    const long v = std::strtol(s, &end, 10);
+    if (*s && *end == 0 && v >= 1 && v <= 4096) d.cus = (int)v;
+  }
+  return d;
+}
+
 // ------------------------------------------------------------- profiling
 namespace {
 // Process-wide profiling state.  The loop reads `period` without a lock;
@@ -392,6 +445,20 @@ size_t fkc_kmeans_workspace_bytes(int64_t B, int64_t N, int64_t K, int64_t D,
   size_t total = 0;
   carve_loop(nullptr, B, N, K, D, dtype, max_iters, &total);
   return total;
+}
+
+size_t fkc_kmeans_sort_recounts_offset(int64_t B, int64_t N, int64_t K,
+                                       int64_t D, int dtype, int max_iters) {
+  if (B <= 0 || N <= 0 || K < 1 || D < 1) return 0;
+  // The recount word is the first int32 of the sort's control region, which
+  // the loop's prologue clears; carving from a non-null base at 0 gives the
+  // offsets (the base is never dereferenced).
+  char* const base = reinterpret_cast<char*>(kWorkspaceAlign);
+  const LoopBuffers L = carve_loop(base, B, N, K, D, dtype, max_iters, nullptr);
+  int32_t* p = nullptr;
+  int64_t n = 0;
+  label_sort_reset_region(L.sort_ws, B, N, K, &p, &n);
+  return n > 0 ? (size_t)(reinterpret_cast<char*>(p) - base) : 0;
 }
 
 }  // extern "C"

@@ -90,6 +90,27 @@ __device__ inline uint32_t lanes_below(uint64_t mask) {
       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
 }
 
+// Handing data to other workgroups of the same launch without a release
+// fence.  The data (a fused sort pass's digit counts, the update's head
+// partials) is written with relaxed agent-scope atomics, which gfx950
+// performs at the device's coherence point, past the CU and XCD caches;
+// the reader loads it with agent-scope atomic loads, performed there too.
+// Before the atomic that announces the data (an arrival counter) the
+// writer waits for its own outstanding vector memory operations: once they
+// have completed they are performed at that point, so a reader that has
+// seen the announcement and then loads with agent scope sees the data.
+// This rests on the hardware's behaviour, not on the HIP memory model,
+// which would ask for a release fence before the announcement and an
+// acquire after it (a release fence writes back the XCD's L2, which cost
+// ~0.1 us per wave at every arrival).  Every site that relies on it calls
+// this helper, so moving to release / acquire (or to another architecture)
+// changes this one place.  The sort and update tests compare both sides of
+// every such hand-over bit for bit against the oracle (and the sort's
+// against its recount fallback, FKC_SORT_SPIN=0).
+__device__ inline void drain_before_announce() {
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // True when the control block says the Lloyd loop already converged.
 __device__ inline bool loop_done(const int32_t* ctrl) {
   return ctrl != nullptr && *ctrl != 0;

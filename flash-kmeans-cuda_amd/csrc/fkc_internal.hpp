@@ -69,6 +69,10 @@ struct SortPlan {
 // the sentinel bin (K = 256 then sorts in one 8-bit pass).
 SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid);
 size_t sort_workspace_bytes(int64_t B, int64_t N, int64_t K);
+// Tiles of this size one launch may hold that all run at once on the
+// current device (CUs x workgroups per CU, capped): grids within it chain
+// by block index and count their digits in the first pass.
+int64_t sort_resident_tiles(int tile);
 // seq < 0: standalone call (clears the workspace's control region first).
 // seq >= 0: the number of earlier calls on this workspace since the caller
 // cleared it with label_sort_reset (0, 1, 2, ... over consecutive calls of
@@ -186,6 +190,21 @@ int lloyd_run(const void* x, const void* init, void* centroids,
               int64_t D, int dtype, int max_iters, float tol, void* workspace,
               size_t workspace_bytes, fkc_stream_t stream,
               int32_t* n_iters_dev, int32_t* n_iters_host, bool profile);
+
+// ---------------------------------------------------------------- device
+// Compute units and the LDS one workgroup may hold on the current device,
+// read with hipDeviceGetAttribute once per device.  The launch plans size
+// their grids from it (workgroups that fill the chip, grids resident at
+// once, centroid tables that fit LDS).  Without a device (a CPU host asking
+// for workspace sizes) the MI355X figures stand in.  FKC_CUS=n overrides
+// the CU count (tests and A/B runs of the plans of a smaller part).
+constexpr int kMi355xCUs = 256;
+constexpr int kMi355xLds = 160 * 1024;
+struct DeviceShape {
+  int cus;
+  int lds_per_wg;
+};
+DeviceShape device_shape();
 
 // FKC_NTILES=1|2|4|8: 16-point tiles per wave in the MFMA kernel; 0 = auto.
 int ntiles_override();

@@ -57,6 +57,9 @@
 #include "device_util.hpp"
 #include "fkc_internal.hpp"
 
+#include <algorithm>
+#include <atomic>
+
 namespace fkc {
 namespace {
 
@@ -71,9 +74,10 @@ constexpr int SPIN_LIMIT = 1 << 18;  // empty polls per wait (< 1 s)
 #define FKC_SORT_LB 4
 #endif
 constexpr int LB = FKC_SORT_LB;      // status words read per look-back step
-// Grids of at most this many tiles (per launch) are resident at once, so a
-// tile may take its block index as its place in the chain and the first
-// pass may wait at a row barrier.
+// Grids of at most this many tiles (per launch), and at most the device
+// holds at once (sort_resident_tiles), are resident at once, so a tile may
+// take its block index as its place in the chain and the first pass may
+// wait at a row barrier.
 constexpr int64_t STATIC_TILES_MAX = 256;
 // Per-row counters (uint64): the tile counter of each pass, then the
 // arrival counter of the fused first pass.
@@ -194,7 +198,7 @@ __device__ inline int2 scan256x2(int a, int c, int* wtot, int tid,
     wtot[wave] = ia;
     wtot[4 + wave] = ic;
   }
-  if (drain) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (drain) drain_before_announce();
   __syncthreads();
   int ba = 0, bc = 0;
   for (int w = 0; w < min(wave, 4); ++w) {
@@ -684,7 +688,54 @@ void launch_onesweep(dim3 grid, hipStream_t s, const SweepArgs& a) {
                      0, s, a);
 }
 
+// Onesweep workgroups of this tile size one CU holds at once (the occupancy
+// API), read once per device; 1 without a device.
+template <int TILE>
+int onesweep_per_cu() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];  // 0: not read yet
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();
+    return 1;
+  }
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void*>(&sort_onesweep_kernel<TILE>),
+            Geom<TILE>::ST, 0) != hipSuccess ||
+        n < 1)
+      n = 1;
+    (void)hipGetLastError();
+    cache[dev].store(n, std::memory_order_relaxed);
+    v = n;
+  }
+  return v;
+}
+
 }  // namespace
+
+// Tiles of one launch that run at once on the current device: its CUs times
+// the onesweep workgroups per CU, capped at STATIC_TILES_MAX.  A grid within
+// it may take block indices as chain positions and wait at a row barrier
+// (every tile it waits for is running); a larger one takes positions from a
+// counter and counts its digits in an upsweep.  A device shared with other
+// work can still hold fewer: the waits are bounded, so that costs time, not
+// correctness (the recount word reports it).
+int64_t sort_resident_tiles(int tile) {
+  int per_cu = 1;
+  switch (tile) {
+    case 256: per_cu = onesweep_per_cu<256>(); break;
+    case 512: per_cu = onesweep_per_cu<512>(); break;
+    case 1024: per_cu = onesweep_per_cu<1024>(); break;
+    case 2048: per_cu = onesweep_per_cu<2048>(); break;
+    case 8192: per_cu = onesweep_per_cu<8192>(); break;
+    default: per_cu = onesweep_per_cu<4096>(); break;
+  }
+  return std::min<int64_t>(STATIC_TILES_MAX,
+                           (int64_t)device_shape().cus * per_cu);
+}
 
 SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
   SortPlan p;
@@ -725,7 +776,8 @@ SortPlan sort_plan(int64_t B, int64_t N, int64_t K, bool labels_valid) {
   const int64_t t2k = (N + 2047) / 2048;
   int tile = B * N <= 16384   ? 512
              : B * N <= 65536 ? 1024
-             : (B > 1 && t2k <= 32 && B * t2k <= STATIC_TILES_MAX) ? 2048
+             : (B > 1 && t2k <= 32 && B * t2k <= sort_resident_tiles(2048))
+                 ? 2048
                               : 4096;
   if (const int o = sort_tile_override()) tile = o;
   p.tile = tile;
@@ -772,7 +824,7 @@ int launch_label_sort(const int32_t* ids, int32_t* sorted_ids, int32_t* perm,
   }
   // A grid that is resident at once takes block indices as tiles and counts
   // the digits in its first pass; a larger one needs the upsweep.
-  const bool resident = B * p.ntiles <= STATIC_TILES_MAX;
+  const bool resident = B * p.ntiles <= sort_resident_tiles(p.tile);
   const bool fuse = resident && sort_fuse_override();
   int rc = FKC_OK;
   if (!fuse) {

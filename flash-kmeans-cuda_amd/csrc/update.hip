@@ -625,7 +625,7 @@ update_runs_kernel(const typename Elem<DT>::T* __restrict__ x,
   if (bfull) {
     // The head partial's atomic stores are performed where the summing
     // wave reads them; waiting for them orders them before the arrival.
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    drain_before_announce();
     const int beta = u / UB;
     int old = 0;
     if (lane == 0)

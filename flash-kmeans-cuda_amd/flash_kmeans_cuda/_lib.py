@@ -50,6 +50,7 @@ SIGNATURES = {
     "fkc_kmeans_lloyd_noalloc": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp, _vp, _vp]),
     "fkc_profile_enable": (None, [_int]),
     "fkc_profile_assign_ms": (_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
+    "fkc_kmeans_sort_recounts_offset": (_sz, [_i64, _i64, _i64, _i64, _int, _int]),
 }
 
 

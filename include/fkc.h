@@ -257,7 +257,11 @@ FKC_CAPI int fkc_kmeans_lloyd_from(const void* x, const void* init_centroids,
  * device current; stream must belong to the current device.  Every call on
  * one GPU shares the array: calls that overlap on one GPU (other streams or
  * host threads) race, so serialise them.  Same results as
- * fkc_kmeans_lloyd_from; the profiling hook is not applied.
+ * fkc_kmeans_lloyd_from; the profiling hook is not applied.  Under HIP graph
+ * capture: make the device's first call outside the capture (it looks the
+ * array up), pass tol <= 0 and n_iters_host = NULL (with tol > 0 filling
+ * n_iters_host synchronises the stream, which capture forbids); n_iters_dev
+ * may be given.
  */
 FKC_CAPI size_t fkc_kmeans_noalloc_max_bytes(void);
 FKC_CAPI int fkc_kmeans_lloyd_noalloc(const void* x, const void* init_centroids,
@@ -282,6 +286,20 @@ FKC_CAPI int fkc_kmeans_lloyd_noalloc(const void* x, const void* init_centroids,
  */
 FKC_CAPI void fkc_profile_enable(int enable);
 FKC_CAPI int fkc_profile_assign_ms(double* total_ms, int64_t* launches);
+
+/*
+ * Diagnostic (no counterpart in the reference): byte offset, inside a
+ * workspace of fkc_kmeans_workspace_bytes(B, N, K, D, dtype, max_iters)
+ * bytes, of an int32 that fkc_kmeans_lloyd* clear at the start of a call and
+ * that counts the label-sort tiles of that call whose bounded wait on other
+ * tiles ran out, so that they recounted from their input instead (the
+ * results are the same either way; a non-zero count means the sort's grid
+ * did not run at once, e.g. on a GPU shared with other work, and cost
+ * time).  Read it after the call has finished (one int32 copy to the host).
+ */
+FKC_CAPI size_t fkc_kmeans_sort_recounts_offset(int64_t B, int64_t N, int64_t K,
+                                                int64_t D, int dtype,
+                                                int max_iters);
 
 #ifdef __cplusplus
 }

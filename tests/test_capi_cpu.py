@@ -247,3 +247,62 @@ def test_sampled_inertia_validation_without_a_device():
     assert need >= 2 * 100 * 40 * 2 + 2 * 100 * 4 + 2 * 7 * 4 + 2 * 100 * 4 + 7 * 4
     assert L.fkc_sampled_inertia_workspace_bytes(0, 100, 7, 40, 2) == 0
     assert L.fkc_sampled_inertia(None, None, None, 0, 0, 0, 4, 8, 1, None, None, 0, None) == 0
+
+
+_PLAN_PROBE = r"""
+import json, sys
+sys.path.insert(0, sys.argv[1])
+from flash_kmeans_cuda import _lib
+L = _lib.lib
+print(json.dumps({
+    "sort_c4": L.fkc_label_sort_workspace_bytes(8, 65536, 1024),
+    "sort_c5": L.fkc_label_sort_workspace_bytes(1, 524288, 8192),
+    "assign_c5s8": L.fkc_euclid_assign_workspace_bytes(1, 65536, 8192, 128, 1),
+    "loop_c4": L.fkc_kmeans_workspace_bytes(8, 65536, 1024, 64, 2, 15),
+}))
+"""
+
+
+def _plan_sizes(cus=None):
+    """Workspace sizes the library plans for, in a fresh process (FKC_CUS:
+    plan as if the device had that many compute units)."""
+    import json
+    import subprocess
+    import sys
+    env = dict(os.environ)
+    env.pop("FKC_CUS", None)
+    if cus is not None:
+        env["FKC_CUS"] = str(cus)
+    r = subprocess.run([sys.executable, "-c", _PLAN_PROBE,
+                        os.path.join(REPO, "flash-kmeans-cuda_amd")],
+                       capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def test_plans_follow_the_device_cu_count():
+    """The grid plans read the device's CU count (MI355X's 256 without a
+    device): 256 CUs keep the MI355X plans; a 64-CU part leaves c4's 256
+    sort tiles of 2048 keys non-resident, so 4096-key tiles (half the status
+    words) are taken, and c5's one-GPU share slices K into fewer centroid
+    slices (3 per CU of 64 CUs over 256 point tiles: none), so its assign
+    needs no slice workspace."""
+    base = _plan_sizes()
+    assert _plan_sizes(256) == base
+    assert base["assign_c5s8"] > 0
+    small = _plan_sizes(64)
+    assert small["sort_c4"] < base["sort_c4"]
+    assert small["assign_c5s8"] == 0
+    assert small["sort_c5"] == base["sort_c5"]  # 128 tiles of 4096 either way
+    assert small["loop_c4"] < base["loop_c4"]
+
+
+def test_sort_recounts_offset_lies_inside_the_loop_workspace():
+    from flash_kmeans_cuda import _lib
+    L = _lib.lib
+    for (B, N, K, D, dt, it) in [(1, 524288, 8192, 128, 1, 10), (8, 65536, 1024, 64, 2, 15),
+                                 (1, 4096, 64, 128, 0, 10), (2, 100, 1, 8, 1, 3)]:
+        off = L.fkc_kmeans_sort_recounts_offset(B, N, K, D, dt, it)
+        total = L.fkc_kmeans_workspace_bytes(B, N, K, D, dt, it)
+        assert 0 < off and off % 256 == 0 and off + 4 <= total
+    assert L.fkc_kmeans_sort_recounts_offset(0, 10, 4, 8, 1, 3) == 0

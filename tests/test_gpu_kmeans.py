@@ -231,6 +231,58 @@ def test_loop_sort_paths_agree(monkeypatch, cfg_name, N):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), (fuse, spin)
 
 
+@pytest.mark.parametrize("cus", ["64", "16"])
+def test_loop_with_the_plans_of_a_smaller_part(monkeypatch, cus):
+    """FKC_CUS plans every grid as for a part with fewer compute units
+    (fewer sort tiles resident at once, so counter-ordered tiles and an
+    upsweep; fewer assign workgroups to fill it, so no centroid slices): the
+    loop gives the same bits as with the device's own plans (c5's shape at
+    N = 262144: 64 sort tiles of 4096 keys, resident on 64 CUs, not on 16;
+    c5's share of one of 8 GPUs: 3 centroid slices on 256 CUs, none on 64 or
+    16; c4's shape at N = 16384)."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    for name, N in [("c5", 262144), ("c5s8", 65536), ("c4", 16384)]:
+        cfg = synth.CONFIGS[name]
+        x, init = synth.make(cfg, N=N)
+        xt, it = _T(x, cfg.dtype), _T(init, cfg.dtype)
+        monkeypatch.delenv("FKC_CUS", raising=False)
+        a = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
+        monkeypatch.setenv("FKC_CUS", cus)
+        b = batch_kmeans_Euclid(xt, cfg.K, max_iters=3, init_centroids=it)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), (name, cus)
+
+
+def test_loop_sort_recount_word_is_zero_on_an_idle_gpu(monkeypatch):
+    """A c5 loop call on an otherwise idle GPU never runs out of a sort wait:
+    the recount word (fkc_kmeans_sort_recounts_offset) reads 0; with
+    FKC_SORT_SPIN=0 every wait gives up at once and it counts them."""
+    from flash_kmeans_cuda import _lib, synth
+    cfg = synth.CONFIGS["c5"]
+    x, init = synth.make(cfg, N=131072)
+    xt, it = _T(x, cfg.dtype), _T(init, cfg.dtype)
+    L = _lib.lib
+    B, N, K, D = 1, 131072, cfg.K, cfg.D
+
+    def run():
+        ws = torch.full((L.fkc_kmeans_workspace_bytes(B, N, K, D, 1, 3),), 0x5A,
+                        dtype=torch.uint8, device="cuda")
+        cents = torch.empty_like(it)
+        ids = torch.empty((B, N), dtype=torch.int32, device="cuda")
+        _lib.check(L.fkc_kmeans_lloyd_from(
+            xt.data_ptr(), it.data_ptr(), cents.data_ptr(), ids.data_ptr(), B, N, K, D, 1,
+            3, 0.0, ws.data_ptr(), ws.numel(), _lib.stream_of(xt), None, None), "lloyd")
+        off = L.fkc_kmeans_sort_recounts_offset(B, N, K, D, 1, 3)
+        torch.cuda.synchronize()
+        return int(ws[off:off + 4].view(torch.int32).item()), ids, cents
+
+    n0, ids0, c0 = run()
+    assert n0 == 0
+    monkeypatch.setenv("FKC_SORT_SPIN", "0")
+    n1, ids1, c1 = run()
+    assert n1 > 0
+    assert torch.equal(ids0, ids1) and torch.equal(c0, c1)
+
+
 @pytest.mark.parametrize("tile", [256, 512])
 def test_loop_with_counter_ordered_sort_tiles(monkeypatch, tile):
     """Sort grids of more than 256 tiles take their tile index from a per-row
