@@ -89,3 +89,72 @@ def test_no_alloc_refuses_shapes_beyond_the_scratch():
     rc = _lib.lib.fkc_kmeans_lloyd_noalloc(fake, fake, fake, fake, B, N, K, D, dt, 10, 0.0,
                                           None, None, None)
     assert rc == 2 and "static scratch" in _lib.last_error()
+
+
+_CAPTURED_NO_ALLOC = r'''
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from flash_kmeans_cuda import _lib
+L = _lib.lib
+for (B, N, K, D, dtype) in [(1, 16384, 256, 128, torch.float16), (2, 8192, 700, 64, torch.bfloat16)]:
+    g = torch.Generator(device="cuda").manual_seed(N + K)
+    x = torch.randn(B, N, D, device="cuda", generator=g).to(dtype)
+    init = x[:, :K].contiguous().clone()
+    keep = init.clone()
+    cents = torch.empty_like(init)
+    ids = torch.empty((B, N), dtype=torch.int32, device="cuda")
+    dt = _lib.dtype_code(dtype)
+    s = torch.cuda.Stream()
+
+    def call():
+        _lib.check(L.fkc_kmeans_lloyd_noalloc(
+            x.data_ptr(), init.data_ptr(), cents.data_ptr(), ids.data_ptr(), B, N, K, D, dt,
+            2, 0.0, s.cuda_stream, None, None), "kmeans_lloyd_noalloc")
+
+    with torch.cuda.stream(s):
+        call()                       # set-up: the scratch array's address
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    with torch.cuda.stream(s):
+        call()                       # a warm call allocates nothing
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free0 == free1, ("device memory changed", free0, free1)
+    e_c, e_i = cents.clone(), ids.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        call()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        cents.fill_(7.0)
+        ids.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cents, e_c) and torch.equal(ids, e_i), ("replay", rep)
+        with torch.cuda.stream(s):
+            call()                   # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(cents, e_c) and torch.equal(ids, e_i), ("eager", rep)
+    assert torch.equal(init, keep)
+print("noalloc-graph-ok", flush=True)
+'''
+
+
+def test_no_alloc_allocates_nothing_and_replays_under_graph_capture():
+    """The entry point's promise, in a fresh process: once set up (first
+    call on the device), a call changes no device memory (hipMemGetInfo's
+    free bytes are the same around it), and with tol <= 0, n_iters_dev and
+    n_iters_host NULL it can be captured into a HIP graph whose replays,
+    with eager calls and synchronisations between them, equal the eager
+    call bit for bit (a c2-like fp16 shape and the bf16 centroid-resident
+    route)."""
+    import os
+    import subprocess
+    import sys
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                       "flash-kmeans-cuda_amd")
+    r = subprocess.run([sys.executable, "-c", _CAPTURED_NO_ALLOC, pkg],
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "noalloc-graph-ok" in r.stdout, (r.stdout[-2000:],
+                                                                    r.stderr[-2000:])
