@@ -209,7 +209,8 @@ def test_tol_stops_at_the_oracles_iteration():
     assert torch.equal(it, _T(init, "bf16")), "init_centroids was modified"
 
 
-@pytest.mark.parametrize("cfg_name,N", [("c3", 65536), ("c2", 32768), ("c4", 8192)])
+@pytest.mark.parametrize("cfg_name,N", [("c3", 65536), ("c2", 32768), ("c4", 8192),
+                                        ("c5", 131072)])
 def test_loop_sort_paths_agree(monkeypatch, cfg_name, N):
     """The Lloyd loop gives the same bits whichever way its sorts count
     digits (in the first pass, or in a separate upsweep: FKC_SORT_FUSE=0)
@@ -336,6 +337,31 @@ def test_few_clusters_many_points(B, N, K, D, dtype):
     assert (a[0].cpu().numpy() != o_ids).mean() < 1e-3
     gc, oc = O.to_f64(_N(a[1], dtype), dtype), O.to_f64(o_c, dtype)
     assert np.linalg.norm(gc - oc) / np.linalg.norm(oc) < 1e-2
+
+
+@pytest.mark.parametrize("B,N,K,D,dtype", [(3, 90000, 700, 128, "f16"), (2, 150000, 300, 64, "bf16"),
+                                           (1, 40000, 4000, 8, "f32")])
+def test_loop_runs_of_every_length(B, N, K, D, dtype):
+    """Zipf-sized clusters (runs from a few rows to tens of thousands:
+    inside one unit, over a few units, over whole 64-unit blocks): the
+    loop, whose update completes every run over several units inside its
+    run kernel, equals the per-op path (separate merge kernel, pinned by
+    the lockstep tests) bit for bit over three iterations; one iteration
+    assigns as the oracle does up to near-ties."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid, synth
+    rng = np.random.default_rng(K + D)
+    centres = 3 * rng.standard_normal((B, K, D)).astype(np.float32)
+    blob = rng.choice(K, (B, N), p=synth.zipf_probs(K, 1.1))
+    x = O.from_f32(np.take_along_axis(centres, blob[..., None], 1)
+                   + 0.5 * rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    init = np.ascontiguousarray(x[:, rng.choice(N, K, replace=False)])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it, verbose=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    one = batch_kmeans_Euclid(xt, K, max_iters=1, init_centroids=it)[0].cpu().numpy()
+    nd, bad, worst = near_tie_report(x, init, dtype, one, O.assign(x, init, dtype))
+    assert bad == 0 and nd / one.size < 1e-3, (nd, bad, worst)
 
 
 @pytest.mark.parametrize("B,N,K,D,dtype", [(1, 200000, 2, 1100, "f16"), (2, 120000, 3, 600, "bf16")])
