@@ -27,33 +27,37 @@
 
 namespace fkc {
 
-// Allocate and return (B, N) int32 cluster ids.
+// Nearest-centroid label of every point, in a new (B, N) int32 tensor.
 FKC_API at::Tensor euclid_assign(const at::Tensor& x, const at::Tensor& centroids,
                                  const at::Tensor& x_sq, const at::Tensor& c_sq);
 
-// Write into caller-provided (B, N) int32 cluster_ids and return it.
+// As euclid_assign, with the labels stored in the caller's (B, N) int32
+// tensor, which is returned.
 FKC_API at::Tensor euclid_assign_out(const at::Tensor& x, const at::Tensor& centroids,
                                      const at::Tensor& x_sq, const at::Tensor& c_sq,
                                      at::Tensor cluster_ids);
 
-// Sorted-run centroid accumulation; centroid_sums / centroid_counts are
-// zeroed here before accumulating.
+// Per-label fp32 row sums and int32 counts over label-sorted rows; the
+// output tensors are cleared first.
 FKC_API void centroid_update_sorted(const at::Tensor& x_sorted,
                                     const at::Tensor& cluster_ids_sorted,
                                     at::Tensor centroid_sums, at::Tensor centroid_counts);
 
-// Same accumulator, reading rows of original-order x through sorted_idx.
+// The same sums and counts with x in its original row order, row p of the
+// sorted order being x[sorted_idx[p]].
 FKC_API void centroid_update_sorted_indexed(const at::Tensor& x, const at::Tensor& sorted_idx,
                                             const at::Tensor& cluster_ids_sorted,
                                             at::Tensor centroid_sums,
                                             at::Tensor centroid_counts);
 
-// Allocate and return finalized centroids.
+// New centroids sums / counts (the old centroid where a count is 0), in a
+// new tensor of old_centroids' dtype.
 FKC_API at::Tensor centroid_finalize(const at::Tensor& centroid_sums,
                                      const at::Tensor& centroid_counts,
                                      const at::Tensor& old_centroids);
 
-// Write finalized centroids into caller-provided out and return it.
+// As centroid_finalize, stored in the caller's tensor `out`, which is
+// returned.
 FKC_API at::Tensor centroid_finalize_out(const at::Tensor& centroid_sums,
                                          const at::Tensor& centroid_counts,
                                          const at::Tensor& old_centroids, at::Tensor out);
