@@ -1255,20 +1255,38 @@ struct Plan {
 // The saved-score fold keeps the best block's four scores per lane, so the
 // winner needs no re-score: the re-score reads four full candidate rows per
 // point (512 B at D = 64, bf16), which at the end of a round of workgroups
-// is all CU-L1 traffic with the matrix cores idle.  Four tiles, unpadded:
-// at D = 97..128 it runs at two waves per SIMD and is taken where the
-// launch has at most two workgroups per CU anyway (grids of <= 512
-// workgroups); at D = 64 it costs a wave per SIMD (163 VGPRs, three waves)
-// and four selects per 16-centroid block, which pays for K (per slice) <=
-// 1024 (same-box assign times against the re-score, bf16: (4, 100000, 600)
-// -25%, (1, 262144, 1024) -9.6%, (8, 65536, 1024) -2.4% to -6.7%; but
-// (8, 65536, 2048) +8.3%, (1, 524288, 2048) +7.6%, K = 4096 / 8192
-// +14 / +15%).  FKC_SAVE=0/1 forces it off / on where it exists.
+// is all CU-L1 traffic with the matrix cores idle.  Four tiles, unpadded.
+// At D = 97..128 it runs two workgroups per CU against the re-score's
+// three, so besides skipping the re-score it changes how whole the rounds
+// of workgroups are: a round that is a fraction of the slots ends with
+// CUs running one workgroup.  It is taken where K (per slice) <= 2048 at
+// any grid, and up to K = 8191 where its rounds are whole enough
+// (round_fill below) to beat the re-score's by 0.15; at K >= 8192 only on
+// grids of at most two workgroups per CU.  Same-box fp16 assign times over
+// grids of 256..1536 workgroups and K = 1024..8192 (N = 256 x workgroups),
+// save against re-score: K = 1024 -24% to -31% from 640 workgroups on,
+// K = 2048 -2% to -17% (c3's 512: +1%), K = 3072 / 4096 at 896 and 1024
+// workgroups -9% / -6% and -5% / -2%, at 640, 768, 1280, 1536 +3% to +9%;
+// K = 8192 at 1024 +3%.  At D = 64 it costs a wave per SIMD (163 VGPRs,
+// three waves) and four selects per 16-centroid block, which pays for K
+// (per slice) <= 1024 (same-box assign times against the re-score, bf16:
+// (4, 100000, 600) -25%, (1, 262144, 1024) -9.6%, (8, 65536, 1024) -2.4% to
+// -6.7%; but (8, 65536, 2048) +8.3%, (1, 524288, 2048) +7.6%, K = 4096 /
+// 8192 +14 / +15%).  FKC_SAVE=0/1 forces it off / on where it exists.
+static double round_fill(int64_t wgs, int64_t slots) {
+  const int64_t rounds = (wgs + slots - 1) / slots;
+  return (double)wgs / (double)(rounds * slots);
+}
+
 static bool use_save(const Plan& p, int64_t wgs) {
   if (p.pt != 4 || (p.ds2 != 4 && p.ds2 != 2) || p.pad || p.exact) return false;
   const int o = save_override();
   if (o >= 0) return o == 1;
-  return p.ds2 == 4 ? wgs <= 512 : p.kspan <= 1024;
+  if (p.ds2 == 2) return p.kspan <= 1024;
+  const int64_t cus = device_shape().cus;
+  if (p.kspan <= 2048) return true;
+  if (p.kspan >= 8192) return wgs <= 2 * cus;
+  return round_fill(wgs, 2 * cus) >= round_fill(wgs, 3 * cus) + 0.15;
 }
 
 // Tiles per wave of the resident kernel.

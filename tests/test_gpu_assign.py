@@ -146,6 +146,35 @@ def test_eight_tiles_match_oracle_and_four(monkeypatch, dtype, B, N, K):
     _check(x, c, dtype, got8, max_frac=1e-3)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("B,N,K,D", [
+    (1, 5000, 1030, 128), (2, 3001, 2100, 128), (1, 9000, 4097, 128),
+    (1, 4000, 1500, 64), (3, 2000, 1300, 64),
+    (1, 262144, 4096, 128), (1, 229376, 3072, 128), (1, 163840, 1024, 128),
+])
+def test_saved_scores_match_rescore(monkeypatch, dtype, B, N, K, D):
+    """The four-tile kernel's two ways of naming the winner -- the scores
+    of each lane's best 16-centroid block kept in registers, or the four
+    candidate rows of that block re-scored after the loop -- give identical
+    labels (same MFMA chain per score, first maximum either way): ragged N,
+    K off the 64-row stage, batches, a K split into slices (4097 rows), and
+    the grids whose plan takes the kept scores for whole rounds (1024 and
+    896 workgroups).  Against the oracle where it finishes in seconds."""
+    x, c = _data(B, N, K, D, dtype, seed=N + K + D)
+    monkeypatch.setenv("FKC_NTILES", "4")
+    outs = []
+    for s in ["0", "1"]:
+        monkeypatch.setenv("FKC_SAVE", s)
+        outs.append(_gpu_assign(x, c, dtype))
+    monkeypatch.delenv("FKC_SAVE")
+    monkeypatch.delenv("FKC_NTILES")
+    outs.append(_gpu_assign(x, c, dtype))  # the plan's own choice
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], outs[2])
+    if B * N * K <= 2e7:
+        _check(x, c, dtype, outs[0], max_frac=1e-3)
+
+
 RESIDENT_CASES = [
     # (B, N, K, D): one centroid, K below and not a multiple of 16, ragged N,
     # batches, c4's shape at reduced N, and the largest tables that fit one
