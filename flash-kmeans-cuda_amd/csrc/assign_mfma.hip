@@ -1234,14 +1234,23 @@ static bool pt8_ok(int ds2, bool pad, bool exact) {
 // budget) whose grid fills the chip (fill_wgs); fewer, fatter workgroups
 // reuse each LDS centroid stage more, but grids that leave CUs idle hide
 // latency badly (measured at the c2..c5 shapes; eight tiles at D = 64 ran
-// slower than four).  FKC_NTILES overrides where the variant exists.
-static int choose_pt(int ds2, bool pad, bool exact, int64_t B, int64_t N) {
+// slower than four).  From K = 8192 one full round of eight-tile
+// workgroups (2 per CU) is enough: their longer loop amortizes the
+// prologue and re-score (fp16, N = 256 x four-tile workgroups, same box,
+// interleaved: 1024 / 1280 / 1536 workgroups' worth of points at
+// K = 8192 -3.3% / -0.4% / -1.3%, at K = 16384 -6.1% / -4.2% / -4.0%;
+// at K = 4096 one or one and a half rounds lose, +8% to +12%).
+// FKC_NTILES overrides where the variant exists.
+static int choose_pt(int ds2, bool pad, bool exact, int64_t B, int64_t N,
+                     int64_t K) {
   const int o = ntiles_override();
   if (o == 8 && pt8_ok(ds2, pad, exact)) return o;
   if (o != 0 && o != 8 && o * ds2 * 4 <= 64) return o;
   for (int pt = 8; pt > 1; pt >>= 1) {
     if (pt == 8 ? !pt8_ok(ds2, pad, exact) : pt * ds2 * 4 > 64) continue;
     if (grid_wgs(pt, B, N) >= fill_wgs(pt, ds2, exact)) return pt;
+    if (pt == 8 && K >= 8192 && grid_wgs(8, B, N) >= 2 * device_shape().cus)
+      return 8;
   }
   return 1;
 }
@@ -1336,7 +1345,7 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
   // (1, 262144, 768, 32) 0.0288 -> 0.0238, (4, 100000, 1000, 48) 0.0752 ->
   // 0.0695).
   p.exact = K <= FKC_EXACT_MAX_K || (p.ds2 <= 2 && K <= FKC_EXACT_MAX_K_NARROW);
-  p.pt = choose_pt(p.ds2, p.pad, p.exact, B, N);
+  p.pt = choose_pt(p.ds2, p.pad, p.exact, B, N, K);
   p.S = 1;
   p.kspan = (int)K;
   if (use_resident(p, B, N, K)) {
