@@ -85,6 +85,12 @@ int update_rows_override() {
   return (v == 32 || v == 64 || v == 128) ? v : 0;
 }
 
+int update_scan_override() {
+  const char* s = std::getenv("FKC_UPDATE_SCAN");
+  if (!s || !*s) return -1;
+  return std::strcmp(s, "1") == 0 ? 1 : (std::strcmp(s, "0") == 0 ? 0 : -1);
+}
+
 bool sort_fuse_override() {
   const char* s = std::getenv("FKC_SORT_FUSE");
   return !(s && std::strcmp(s, "0") == 0);
@@ -506,6 +512,7 @@ int lloyd_run(const void* x, const void* init, void* centroids,
 
   const bool check = tol > 0.f;
   const int32_t* ctrl = check ? L.ctrl : nullptr;
+  const bool scan = update_scan_ok(B, N, K, D);
   // One prologue launch: copy of the initial centroids (when separate),
   // their c_sq, and the zeroing of the control words, the sort's and the
   // update's control regions and the shift slots.
@@ -556,14 +563,20 @@ int lloyd_run(const void* x, const void* init, void* centroids,
         g_prof.stops.push_back(e1);
       }
     }
-    if (!rc)
-      rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
-                             L.sort_ws, L.sort_ws_bytes, ctrl, s, it);
     // The update finalizes the centroids itself when D <= 512 (no sums /
-    // counts round trip); otherwise finalize runs as its own kernel.
+    // counts round trip); otherwise finalize runs as its own kernel.  Short
+    // rows take the sort-free update: one launch, the same bits.
     const UpdateFinalize fin{centroids, L.c_sq, check ? L.shift + it : nullptr};
     bool fused = false;
-    if (!rc)
+    if (!rc && scan) {
+      rc = launch_update_scan(x, cluster_ids, B, N, K, D, dtype, L.upd_ws,
+                              L.upd_ws_bytes, ctrl, s, fin);
+      fused = true;
+    }
+    if (!rc && !scan)
+      rc = launch_label_sort(cluster_ids, L.sorted, L.perm, B, N, K, true,
+                             L.sort_ws, L.sort_ws_bytes, ctrl, s, it);
+    if (!rc && !scan)
       rc = launch_update(x, L.perm, L.sorted, L.sums, L.counts, B, N, K, D,
                          dtype, true, L.upd_ws, L.upd_ws_bytes, ctrl, s, &fin,
                          &fused, it);

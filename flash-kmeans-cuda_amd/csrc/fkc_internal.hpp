@@ -123,6 +123,17 @@ int launch_update(const void* x, const int32_t* perm /*nullable*/,
                   const int32_t* ctrl, hipStream_t s,
                   const UpdateFinalize* fin = nullptr, bool* fused = nullptr,
                   int64_t seq = -1);
+// Sort-free update of the Lloyd loop (no label sort, one launch) for short
+// rows: whether the plan takes it for this shape (FKC_UPDATE_SCAN=0|1 turns
+// it off / on where it can run), and its launch.  Overwrite mode with the
+// finalize fused, every label in [0,K); `ws` is an update workspace
+// (update_workspace_bytes); the centroids, c_sq and shift equal those of
+// launch_label_sort + launch_update bit for bit.
+bool update_scan_ok(int64_t B, int64_t N, int64_t K, int64_t D);
+int launch_update_scan(const void* x, const int32_t* ids, int64_t B,
+                       int64_t N, int64_t K, int64_t D, int dtype, void* ws,
+                       size_t ws_bytes, const int32_t* ctrl, hipStream_t s,
+                       const UpdateFinalize& fin);
 // The int32 region of an update workspace that a sequenced caller zeroes
 // before its first call: *p, *n (n = 0 when B * N == 0).
 void update_control_region(void* ws, int64_t B, int64_t N, int64_t D,
@@ -219,5 +230,8 @@ int resident_override();
 // FKC_UPDATE_ROWS=32|64|128: sorted rows per unit of the centroid update;
 // 0 = auto.
 int update_rows_override();
+// FKC_UPDATE_SCAN=0|1: sort-free loop update off / on where it can run;
+// -1 = auto.
+int update_scan_override();
 
 }  // namespace fkc

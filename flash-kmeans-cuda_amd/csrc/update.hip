@@ -49,6 +49,7 @@
 #include "fkc_internal.hpp"
 
 #include <limits.h>
+#include <cstdlib>
 
 #include <type_traits>
 
@@ -809,6 +810,420 @@ update_merge_kernel(const float* __restrict__ part,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Sort-free update of the Lloyd loop for short rows (update_scan).
+//
+// With N <= SCAN_NMAX points per row the loop replaces its three launches
+// after the assign (label sort, update_runs, update_merge) by one.  Each
+// workgroup owns `kpw` consecutive labels of one batch row.  It reads the
+// whole row of labels into registers (256-label chunks in index order
+// across its waves), counting the labels below its first one and, per
+// chunk, each of its own by ballots; an exclusive prefix over the chunks
+// (one wave per owned label) then gives every owned row its sorted
+// position: the stable sort's order is label-major, index-minor, so a
+// workgroup can place its own rows without sorting anything else.  Each
+// owned row writes its point index at its sorted position in LDS (a window
+// of SCAN_CAP positions at a time).  From there the sums follow the sort
+// path's units and order bit for bit: sorted positions are cut into units
+// of `ur` rows (choose_ur), each piece of a run inside one unit is summed
+// row by row in sorted order from zero, a run inside one unit is finalized
+// at once, and a longer run
+// keeps its tail partial (first unit) and head partials (later units) in
+// the update workspace, then sums full 64-unit blocks and the run itself by
+// wave_ordered_sum in update_merge's item order (tail, heads of the start
+// block, block partials, heads of the end block), so the centroids, c_sq
+// and shift equal those of label_sort + update_runs + update_merge.
+// Every workgroup reads the whole row of labels, so the plan (update_scan_ok)
+// takes this route only for short rows and few labels per workgroup; a row
+// whose rows crowd into a few labels makes their owners sum them alone.
+constexpr int SCAN_NMAX = 32768;   // labels of a row (held in registers)
+constexpr int SCAN_KPW = 16;       // labels owned per workgroup, at most
+constexpr int SCAN_CAP = 16384;    // sorted positions per placement window
+constexpr int SCAN_T = 1024;       // threads per workgroup (16 waves)
+constexpr int SCAN_W = SCAN_T / 64;
+constexpr int SCAN_UMAX = SCAN_NMAX / (4 * SCAN_T);  // label quads per thread
+constexpr int SCAN_CH = SCAN_UMAX * SCAN_W;          // 256-label chunks, at most
+constexpr int SCAN_LIST = 1024;  // owned rows ranked in a list, at most
+
+// SCAN_U: label quads per thread (N <= 4 * SCAN_T * SCAN_U).
+template <int DT, int VEC, int NI, int SCAN_U>
+__global__ void __launch_bounds__(SCAN_T)
+update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
+                   const int32_t* __restrict__ ids, float* __restrict__ part,
+                   float* __restrict__ bpart, int N, int K, int D, int nunits,
+                   int nblocks, int ur, int kpw, int vec4,
+                   FinArgs<typename Elem<DT>::T> fin,
+                   const int32_t* __restrict__ ctrl) {
+  using T = typename Elem<DT>::T;
+  using RC = RawCols<DT, VEC>;
+  using R = typename RC::T;
+  __shared__ uint16_t s_perm[SCAN_CAP];
+  __shared__ float s_row[SCAN_W][FIN_DMAX];
+  // Per 256-label chunk (u, wave) and owned label j: its rows in the chunk,
+  // then their place among the label's rows (exclusive prefix over chunks).
+  __shared__ int s_tab[SCAN_CH][SCAN_KPW];
+  __shared__ __attribute__((aligned(16))) int s_list[SCAN_LIST];
+  __shared__ int s_cnt[SCAN_KPW];
+  __shared__ int s_off[SCAN_KPW + 1];
+  __shared__ int s_red[SCAN_W];
+  __shared__ int s_n;
+  if (loop_done(ctrl)) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.y;
+  const int k0 = blockIdx.x * kpw;
+  const int nk = min(kpw, K - k0);  // >= 1: the grid covers K exactly
+  const int32_t* ib = ids + (size_t)b * N;
+  const T* xb = x + (size_t)b * N * D;
+  float* partb = part + (size_t)b * nunits * 2 * D;
+  float* bpartb = bpart + (size_t)b * nblocks * D;
+
+  for (int i = tid; i < SCAN_CH * SCAN_KPW; i += SCAN_T) (&s_tab[0][0])[i] = 0;
+  if (tid < SCAN_KPW) s_cnt[tid] = 0;
+  if (tid == 0) s_n = 0;
+
+  // 1. The row's labels stay in registers: thread t holds labels
+  // 4 (t + SCAN_T u) + c, u < SCAN_U, c < 4, so for each u the workgroup
+  // covers SCAN_T * 4 consecutive labels in (wave, lane, c) order and the
+  // chunks (u, wave) of 256 labels run in index order.  All loads are in
+  // flight before any is used; -1 past N.
+  int lab[SCAN_U][4];
+#pragma unroll
+  for (int u = 0; u < SCAN_U; ++u) {
+    const int i0 = 4 * (tid + SCAN_T * u);
+    if (vec4 && i0 + 3 < N) {
+      const int4 v = *reinterpret_cast<const int4*>(ib + i0);
+      lab[u][0] = v.x;
+      lab[u][1] = v.y;
+      lab[u][2] = v.z;
+      lab[u][3] = v.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) lab[u][c] = i0 + c < N ? ib[i0 + c] : -1;
+    }
+  }
+  int below = 0;
+#pragma unroll
+  for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) below += (lab[u][c] >= 0 && lab[u][c] < k0) ? 1 : 0;
+  below = wave_sum_i(below);
+  if (lane == 0) s_red[wave] = below;
+
+  int col[NI];
+  bool cok[NI];
+  int lcol[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    col[i] = (lane + 64 * i) * VEC;
+    cok[i] = col[i] < D;
+    lcol[i] = cok[i] ? col[i] : 0;
+  }
+  using Acc = float[NI][VEC];
+  // Rows in flight per wave: 32 raw words, 16 where a raw load is 8 bytes
+  // (fp32 pairs), so the gather fits beside the labels in 128 registers.
+  constexpr int RB = (sizeof(R) >= 8 ? 16 : 32) / NI;
+
+  // Finalize label k0 + j from a row of sums in this wave's LDS row.
+  auto finish = [&](int j, int cnt) {
+    wave_lds_sync();
+    const int id = k0 + j;
+    finalize_row<DT>(s_row[wave], cnt, fin.cent + ((size_t)b * K + id) * D,
+                     fin.c_sq + (size_t)b * K + id, fin.shift, D, lane);
+    wave_lds_sync();
+  };
+
+  // Sum the pieces of owned runs in sorted positions [W0, W1) (W0 a unit
+  // boundary, s_perm holding their point indices): each unit of the window,
+  // each owned run in it; units go to the waves in turn.  A run inside one
+  // unit is finalized at once; a longer run's pieces go to the workspace.
+  auto pieces = [&](int W0, int W1) {
+    const int S0 = s_off[0];
+    for (int u = W0 / ur + wave; u * ur < W1; u += SCAN_W) {
+      const int pa = max(u * ur, S0), pb = min((u + 1) * ur, W1);
+      for (int j = 0; j < nk; ++j) {
+        const int s = s_off[j], e = s_off[j + 1];
+        const int a = max(pa, s), z = min(pb, e);
+        if (a >= z) continue;
+        Acc acc;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[i][v] = 0.f;
+        for (int r0 = a; r0 < z; r0 += RB) {
+          R raw[RB][NI];
+#pragma unroll
+          for (int jj = 0; jj < RB; ++jj) {
+            const int r = min(r0 + jj, z - 1);
+            // (min: a row index stays inside the batch row whatever LDS holds)
+            const int idx = min(__builtin_amdgcn_readfirstlane((int)s_perm[r - W0]), N - 1);
+            const T* row = xb + (size_t)idx * D;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) raw[jj][i] = RC::load(row + lcol[i]);
+          }
+#pragma unroll
+          for (int jj = 0; jj < RB; ++jj) {
+            if (r0 + jj < z) {
+#pragma unroll
+              for (int i = 0; i < NI; ++i) {
+                float f[VEC];
+                RC::cvt(raw[jj][i], f);
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) acc[i][v] = acc[i][v] + f[v];
+              }
+            }
+          }
+        }
+        const int us = s / ur, ue = (e - 1) / ur;
+        float* dst = us == ue ? s_row[wave]
+                              : partb + ((size_t)u * 2 + (u == us ? 1 : 0)) * D;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          if (cok[i]) {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) dst[col[i] + v] = acc[i][v];
+          }
+        if (us == ue) finish(j, e - s);
+      }
+    }
+    __syncthreads();
+  };
+
+  __syncthreads();  // s_tab, s_cnt, s_n cleared; s_red written
+  int S0 = 0;
+#pragma unroll
+  for (int w = 0; w < SCAN_W; ++w) S0 += s_red[w];
+  const int W0 = S0 / ur * ur;
+
+  // 2. The owned rows into a list, key (j << 15) | index: each lane counts
+  // its own, a wave prefix gives its slots and one LDS atomic per wave the
+  // wave's base (the list's order does not matter: it is ranked next).
+  int mine = 0;
+#pragma unroll
+  for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) mine += (unsigned)(lab[u][c] - k0) < (unsigned)nk ? 1 : 0;
+  int incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  const int wtot = __shfl(incl, 63, 64);
+  if (wtot > 0) {  // wave-uniform
+    int base = 0;
+    if (lane == 0) base = atomicAdd(&s_n, wtot);
+    int slot = __builtin_amdgcn_readfirstlane(base) + incl - mine;
+#pragma unroll
+    for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const unsigned j = (unsigned)(lab[u][c] - k0);
+        if (j < (unsigned)nk) {
+          if (slot < SCAN_LIST)
+            s_list[slot] = (int)(j << 15) | (4 * (tid + SCAN_T * u) + c);
+          ++slot;
+        }
+      }
+  }
+  __syncthreads();
+  const int M = s_n;
+  if (M == 0) return;  // every owned label is empty: its centroid stands
+
+  if (M <= SCAN_LIST) {
+    // 3a. A row's place among the owned rows is the number of smaller keys
+    // (keys are distinct); its sorted position is S0 plus that.  The list
+    // is read four keys at a time (every lane the same words: broadcasts).
+    const int4* l4 = reinterpret_cast<const int4*>(s_list);
+    for (int e = tid; e < M; e += SCAN_T) {
+      const int key = s_list[e];
+      int r = 0;
+      const int m4 = M / 4;
+      int f = 0;
+      for (; f + 8 <= m4; f += 8) {  // eight reads in flight
+        int4 q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = l4[f + i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          r += (q[i].x < key) + (q[i].y < key) + (q[i].z < key) + (q[i].w < key);
+      }
+      for (; f < m4; ++f) {
+        const int4 q = l4[f];
+        r += (q.x < key) + (q.y < key) + (q.z < key) + (q.w < key);
+      }
+      for (int g = 4 * m4; g < M; ++g) r += s_list[g] < key;
+      s_perm[S0 + r - W0] = (uint16_t)(key & 0x7fff);
+      atomicAdd(&s_cnt[key >> 15], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int base = S0;
+      for (int j = 0; j < nk; ++j) {
+        s_off[j] = base;
+        base += s_cnt[j];
+      }
+      s_off[nk] = base;
+    }
+    __syncthreads();
+    pieces(W0, S0 + M);
+  } else {
+    // 3b. Too many owned rows for the list: walk the chunks in index order.
+    // Visit the owned labels of chunk (u, this wave) one value at a time
+    // (only the values present): fn(j, pre, tot, mine) with pre the rows of
+    // label k0 + j in lower lanes, tot the chunk's, mine[c] this lane's.
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    auto for_owned = [&](int u, auto fn) {
+      bool pend[4];
+      bool any = false;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pend[c] = (unsigned)(lab[u][c] - k0) < (unsigned)nk;
+        any |= pend[c];
+      }
+      for (;;) {
+        const uint64_t m = __builtin_amdgcn_ballot_w64(any);
+        if (m == 0) break;
+        const int first = pend[0] ? lab[u][0]
+                          : pend[1] ? lab[u][1]
+                          : pend[2] ? lab[u][2] : lab[u][3];
+        const int v = __builtin_amdgcn_readlane(first, (int)__builtin_ctzll(m));
+        bool mine[4];
+        int cj = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          mine[c] = pend[c] && lab[u][c] == v;
+          cj += mine[c] ? 1 : 0;
+          pend[c] = pend[c] && !mine[c];
+        }
+        any = pend[0] || pend[1] || pend[2] || pend[3];
+        const uint64_t m0 = __builtin_amdgcn_ballot_w64(cj & 1);
+        const uint64_t m1 = __builtin_amdgcn_ballot_w64(cj & 2);
+        const uint64_t m2 = __builtin_amdgcn_ballot_w64(cj & 4);
+        const int pre = __builtin_popcountll(m0 & lt) +
+                        2 * __builtin_popcountll(m1 & lt) +
+                        4 * __builtin_popcountll(m2 & lt);
+        const int tot = __builtin_popcountll(m0) + 2 * __builtin_popcountll(m1) +
+                        4 * __builtin_popcountll(m2);
+        fn(v - k0, pre, tot, mine);
+      }
+    };
+#pragma unroll
+    for (int u = 0; u < SCAN_U; ++u)
+      for_owned(u, [&](int j, int, int tot, const bool*) {
+        if (lane == 0) s_tab[u * SCAN_W + wave][j] = tot;
+      });
+    __syncthreads();
+    // Wave j turns label k0 + j's chunk counts into exclusive prefixes
+    // (two chunks per lane) and its total.
+    if (wave < nk) {
+      const int j = wave;
+      const int e0 = s_tab[2 * lane][j], e1 = s_tab[2 * lane + 1][j];
+      int x0 = e0 + e1;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x0, d, 64);
+        if (lane >= d) x0 += y;
+      }
+      const int excl = x0 - e0 - e1;
+      s_tab[2 * lane][j] = excl;
+      s_tab[2 * lane + 1][j] = excl + e0;
+      if (lane == 63) s_cnt[j] = x0;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int base = S0;
+      for (int j = 0; j < nk; ++j) {
+        s_off[j] = base;
+        base += s_cnt[j];
+      }
+      s_off[nk] = base;
+    }
+    __syncthreads();
+    const int S1 = s_off[nk];
+    // Windows of SCAN_CAP sorted positions, starting at a unit boundary: a
+    // row's sorted position is its label's first position, plus its
+    // label's rows in earlier chunks, in lower lanes of its chunk, and in
+    // lower c of its lane.
+    for (int w0 = W0; w0 < S1; w0 += SCAN_CAP) {
+      const int w1 = min(w0 + SCAN_CAP, S1);
+#pragma unroll
+      for (int u = 0; u < SCAN_U; ++u)
+        for_owned(u, [&](int j, int pre, int, const bool* mine) {
+          int p = s_off[j] + s_tab[u * SCAN_W + wave][j] + pre;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (mine[c]) {
+              if (p >= w0 && p < w1)
+                s_perm[p - w0] = (uint16_t)(4 * (tid + SCAN_T * u) + c);
+              ++p;
+            }
+        });
+      __syncthreads();
+      pieces(w0, w1);
+    }
+  }
+
+  // 4. Runs over several units: full 64-unit blocks first (update_runs'
+  // block sums), then each run in update_merge's item order.
+  auto run_items = [&](int s, int e, int& n1, int& beta0, int& nblk, int& v3,
+                       int& n3) {
+    const int us = s / ur, ue = (e - 1) / ur;
+    const int bend = min((us / UB + 1) * UB, nunits);
+    beta0 = us / UB + 1;
+    nblk = 0;
+    n3 = 0;
+    v3 = 0;
+    if (ue < bend) {
+      n1 = ue - us;
+      return;
+    }
+    n1 = bend - (us + 1);
+    int be = beta0;
+    while ((int64_t)(be + 1) * UB * ur < e) ++be;  // blocks wholly inside
+    nblk = be - beta0;
+    v3 = be * UB;
+    n3 = ue - v3 + 1;
+  };
+  for (int j = wave; j < nk; j += SCAN_W) {
+    const int s = s_off[j], e = s_off[j + 1];
+    if (e - s == 0 || s / ur == (e - 1) / ur) continue;
+    int n1, beta0, nblk, v3, n3;
+    run_items(s, e, n1, beta0, nblk, v3, n3);
+    for (int q = 0; q < nblk; ++q) {
+      const int beta = beta0 + q;
+      auto row = [&](int i) {
+        return partb + ((size_t)(beta * UB + i) * 2 + 0) * D;
+      };
+      float* dst = bpartb + (size_t)beta * D;
+      if (D % 4 == 0)
+        wave_ordered_sum<4>(nullptr, UB, 0, D, row, dst, 0, lane);
+      else
+        wave_ordered_sum<1>(nullptr, UB, 0, D, row, dst, 0, lane);
+    }
+  }
+  __syncthreads();
+  for (int j = wave; j < nk; j += SCAN_W) {
+    const int s = s_off[j], e = s_off[j + 1];
+    if (e - s == 0 || s / ur == (e - 1) / ur) continue;
+    int n1, beta0, nblk, v3, n3;
+    run_items(s, e, n1, beta0, nblk, v3, n3);
+    const int us = s / ur;
+    auto row = [&](int i) -> const float* {
+      if (i < n1) return partb + ((size_t)(us + 1 + i) * 2 + 0) * D;
+      if (i < n1 + nblk) return bpartb + (size_t)(beta0 + i - n1) * D;
+      return partb + ((size_t)(v3 + i - n1 - nblk) * 2 + 0) * D;
+    };
+    const float* tail = partb + ((size_t)us * 2 + 1) * D;
+    const int n = n1 + nblk + n3;
+    if (D % 4 == 0)
+      wave_ordered_sum<4>(tail, n, 0, D, row, s_row[wave], 0, lane);
+    else
+      wave_ordered_sum<1>(tail, n, 0, D, row, s_row[wave], 0, lane);
+    finish(j, e - s);
+  }
+}
+
 // Column slices per lane pass: VEC columns per lane (2 when D is even), NI
 // slices of 64 lanes per row (1, 2 or 4), and grid.z column blocks beyond.
 inline int runs_vec(int64_t D) { return row_vec((int)D); }
@@ -927,6 +1342,60 @@ int launch_update_t(const void* x, const int32_t* perm,
   return check_launch("update_merge");
 }
 
+template <int DT, int VEC, int NI>
+int launch_scan_t(const void* x, const int32_t* ids, const UpdateBufs& w,
+                  int64_t B, int64_t N, int64_t K, int64_t D, int kpw,
+                  int vec4, const UpdateFinalize& f, const int32_t* ctrl,
+                  hipStream_t s) {
+  using T = typename Elem<DT>::T;
+  FinArgs<T> fa{static_cast<T*>(f.cent), f.c_sq, f.shift};
+  dim3 grid((unsigned)((K + kpw - 1) / kpw), (unsigned)B);
+  // Two register budgets for the row's labels: rows up to 8192 hold two
+  // quads per thread, longer ones SCAN_UMAX.
+  if (N <= 8 * SCAN_T)
+    hipLaunchKernelGGL((update_scan_kernel<DT, VEC, NI, 2>), grid, dim3(SCAN_T),
+                       0, s, static_cast<const T*>(x), ids, w.part, w.bpart,
+                       (int)N, (int)K, (int)D, (int)w.nunits, (int)w.nblocks,
+                       choose_ur(B, N), kpw, vec4, fa, ctrl);
+  else
+    hipLaunchKernelGGL((update_scan_kernel<DT, VEC, NI, SCAN_UMAX>), grid,
+                       dim3(SCAN_T), 0, s, static_cast<const T*>(x), ids,
+                       w.part, w.bpart, (int)N, (int)K, (int)D,
+                       (int)w.nunits, (int)w.nblocks, choose_ur(B, N), kpw,
+                       vec4, fa, ctrl);
+  return check_launch("update_scan");
+}
+
+template <int DT>
+int launch_scan_dt(const void* x, const int32_t* ids, const UpdateBufs& w,
+                   int64_t B, int64_t N, int64_t K, int64_t D, int kpw,
+                   int vec4, const UpdateFinalize& f, const int32_t* ctrl,
+                   hipStream_t s) {
+#define FKC_SCAN(V, NI_) \
+  return launch_scan_t<DT, V, NI_>(x, ids, w, B, N, K, D, kpw, vec4, f, ctrl, s)
+  const int vec = runs_vec(D), ni = runs_ni(D);
+  if (vec == 2) {
+    if (ni == 1) FKC_SCAN(2, 1);
+    if (ni == 2) FKC_SCAN(2, 2);
+    FKC_SCAN(2, 4);
+  }
+  if (ni == 1) FKC_SCAN(1, 1);
+  if (ni == 2) FKC_SCAN(1, 2);
+  FKC_SCAN(1, 4);
+#undef FKC_SCAN
+}
+
+// Labels per workgroup of update_scan: the row's K labels spread so that
+// the launch has about one workgroup per compute unit.
+int64_t scan_kpw(int64_t B, int64_t K) {
+  if (const char* e = std::getenv("FKC_SCAN_WGS")) {
+    const int64_t w = std::atoll(e);
+    if (w > 0) return (B * K + w - 1) / w;
+  }
+  const int64_t cus = device_shape().cus;
+  return (B * K + cus - 1) / cus;
+}
+
 }  // namespace
 
 size_t update_workspace_bytes(int64_t B, int64_t N, int64_t D) {
@@ -996,6 +1465,55 @@ int launch_update(const void* x, const int32_t* perm,
     }
     default:
       return fail(FKC_ERR_INVALID, "centroid_update: unknown dtype %d", dtype);
+  }
+}
+
+bool update_scan_ok(int64_t B, int64_t N, int64_t K, int64_t D) {
+  const int o = update_scan_override();
+  if (o == 0) return false;
+  if (B < 1 || N < 1 || N > SCAN_NMAX || K < 1 || K > 65535) return false;
+  if (D < 1 || D > FIN_DMAX || D > (int64_t)64 * runs_vec(D) * runs_ni(D))
+    return false;
+  if (scan_kpw(B, K) > SCAN_KPW) return false;
+  // Taken on its own for rows of at most 8192 points, where it measured
+  // faster than the three launches it replaces (loop time per iteration,
+  // same box, random rows, scan vs sort: (1, 2048, 64, 128) f16 14.2 vs
+  // 20.9 us, c1's (1, 4096, 64, 128) f32 20.0 vs 25.0, (1, 4096, 256, 128)
+  // 16.9 vs 25.2, (1, 8192, 256, 128) 17.7 vs 25.8, (1, 8192, 1024, 64)
+  // bf16 23.8 vs 33.9, (4, 8192, 128, 64) 18.6 vs 21.7).  Every workgroup
+  // walks its whole row of labels and each label's rows are summed by their
+  // owner alone, so longer rows gain less and lose where labels crowd: c2's
+  // (1, 32768, 256, 128), whose largest cluster holds 550 rows, 33.7 vs
+  // 29.7 us (random rows of that shape: 24.6 vs 27.8); (1, 16384, 64, 32)
+  // 21.0 vs 20.2.
+  return o == 1 || (N <= 8192 && N <= 256 * K);
+}
+
+int launch_update_scan(const void* x, const int32_t* ids, int64_t B,
+                       int64_t N, int64_t K, int64_t D, int dtype, void* ws,
+                       size_t ws_bytes, const int32_t* ctrl, hipStream_t s,
+                       const UpdateFinalize& fin) {
+  if (!update_scan_ok(B, N, K, D))
+    return fail(FKC_ERR_UNSUPPORTED, "update_scan: shape outside its plan");
+  const size_t need = update_workspace_bytes(B, N, D);
+  if (ws == nullptr || ws_bytes < need)
+    return fail(FKC_ERR_WORKSPACE, "update_scan: workspace %zu < %zu bytes",
+                ws_bytes, need);
+  if (fin.cent == nullptr || fin.c_sq == nullptr)
+    return fail(FKC_ERR_INVALID, "update_scan: no centroids to finalize");
+  const UpdateBufs w = carve_update(ws, B, N, D);
+  const int kpw = (int)scan_kpw(B, K);
+  const int vec4 =
+      (N % 4 == 0 && reinterpret_cast<uintptr_t>(ids) % 16 == 0) ? 1 : 0;
+  switch (dtype) {
+    case FKC_F32:
+      return launch_scan_dt<FKC_F32>(x, ids, w, B, N, K, D, kpw, vec4, fin, ctrl, s);
+    case FKC_F16:
+      return launch_scan_dt<FKC_F16>(x, ids, w, B, N, K, D, kpw, vec4, fin, ctrl, s);
+    case FKC_BF16:
+      return launch_scan_dt<FKC_BF16>(x, ids, w, B, N, K, D, kpw, vec4, fin, ctrl, s);
+    default:
+      return fail(FKC_ERR_INVALID, "update_scan: unknown dtype %d", dtype);
   }
 }
 

@@ -1,0 +1,107 @@
+"""The Lloyd loop's sort-free update for short rows (update_scan) against the
+sort path it replaces (label_sort + update_runs + update_merge): the loop run
+with FKC_UPDATE_SCAN=1 and =0 must give the same labels, centroids and
+iteration counts bit for bit, and the per-op (verbose) path the same again.
+
+Cases: the c1 / c2 shapes the plan takes it for, batches, ragged N (labels
+read one by one instead of four at a time), odd and wide feature widths
+(one to four column slices per lane, two columns per lane or one), several
+labels per workgroup, empty clusters, one point, tol > 0, and rows whose
+points crowd into a few labels: runs over many units, whole 64-unit blocks
+summed as block partials, and a label with more rows than one placement
+window holds.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kmeans_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _T(a, dtype):
+    from flash_kmeans_cuda import synth
+    return synth.to_torch(a, dtype)
+
+
+def _both(monkeypatch, xt, K, init, iters, tol=0.0):
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    out = []
+    for v in ["1", "0"]:
+        monkeypatch.setenv("FKC_UPDATE_SCAN", v)
+        out.append(batch_kmeans_Euclid(xt, K, max_iters=iters, tol=tol,
+                                       init_centroids=init))
+    monkeypatch.delenv("FKC_UPDATE_SCAN")
+    return out
+
+
+def _same(a, b, what):
+    assert a[2] == b[2], (what, "iterations", a[2], b[2])
+    assert torch.equal(a[0], b[0]), (what, "labels")
+    assert torch.equal(a[1], b[1]), (what, "centroids")
+
+
+@pytest.mark.parametrize("B,N,K,D,dtype", [
+    (1, 32768, 256, 128, "f16"),     # c2
+    (1, 4096, 64, 128, "f32"),       # c1
+    (3, 5000, 100, 64, "bf16"),
+    (2, 4099, 37, 96, "f16"),        # N % 4 != 0
+    (1, 3001, 50, 7, "f32"),         # odd D: one column per lane
+    (1, 2000, 20, 512, "f16"),       # four column slices
+    (2, 2500, 30, 300, "bf16"),
+    (1, 20000, 1000, 32, "f16"),     # four labels per workgroup
+    (16, 2048, 200, 16, "f32"),      # thirteen labels per workgroup
+    (1, 1, 1, 16, "f16"),
+    (2, 70, 64, 8, "bf16"),          # most clusters empty
+])
+def test_scan_update_equals_sort_path(monkeypatch, B, N, K, D, dtype):
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    print(f"B={B} N={N} K={K} D={D} {dtype}", flush=True)
+    rng = np.random.default_rng(N + K + D)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32) * 2, dtype)
+    init = np.ascontiguousarray(x[:, rng.choice(N, min(K, N), replace=False)])
+    if init.shape[1] < K:  # more clusters than points: repeat rows
+        init = np.ascontiguousarray(np.concatenate(
+            [init, np.repeat(init[:, :1], K - init.shape[1], axis=1)], axis=1))
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a, b = _both(monkeypatch, xt, K, it, 3)
+    _same(a, b, "scan vs sort")
+    c = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it, verbose=True)
+    _same(a, c, "loop vs per-op path")
+
+
+@pytest.mark.parametrize("B,N,K,D,dtype,share", [
+    (1, 32768, 64, 64, "bf16", 0.95),   # one label with ~31000 rows: two windows
+    (2, 30000, 300, 128, "f16", 0.6),
+    (1, 9000, 40, 24, "f32", 0.9),
+])
+def test_scan_update_crowded_labels(monkeypatch, B, N, K, D, dtype, share):
+    """Most points sit on one centroid: its run covers hundreds of units and
+    whole 64-unit blocks, and (first case) more sorted positions than one
+    placement window (16384)."""
+    print(f"B={B} N={N} K={K} D={D} {dtype} share={share}", flush=True)
+    rng = np.random.default_rng(K + N)
+    x = rng.standard_normal((B, N, D)).astype(np.float32) * 4
+    crowd = rng.random((B, N)) < share
+    x[crowd] = rng.standard_normal((int(crowd.sum()), D)).astype(np.float32) * 0.01
+    x = O.from_f32(x, dtype)
+    init = np.ascontiguousarray(x[:, :K])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a, b = _both(monkeypatch, xt, K, it, 3)
+    _same(a, b, "scan vs sort")
+    counts = np.bincount(a[0].cpu().numpy()[0], minlength=K)
+    assert counts.max() > 0.5 * share * N
+
+
+def test_scan_update_with_tol(monkeypatch):
+    from flash_kmeans_cuda import synth
+    cfg = synth.CONFIGS["c2"]
+    x, init = synth.make(cfg, N=16384)
+    xt, it = _T(x, "f16"), _T(init, "f16")
+    a, b = _both(monkeypatch, xt, cfg.K, it, 30, tol=1e-3)
+    _same(a, b, "tol")
+    assert a[2] < 30
