@@ -91,6 +91,13 @@ int update_scan_override() {
   return std::strcmp(s, "1") == 0 ? 1 : (std::strcmp(s, "0") == 0 ? 0 : -1);
 }
 
+int scan_wgs_override() {
+  const char* s = std::getenv("FKC_SCAN_WGS");
+  if (!s) return 0;
+  const int v = std::atoi(s);
+  return (v >= 1 && v <= 65536) ? v : 0;
+}
+
 bool sort_fuse_override() {
   const char* s = std::getenv("FKC_SORT_FUSE");
   return !(s && std::strcmp(s, "0") == 0);

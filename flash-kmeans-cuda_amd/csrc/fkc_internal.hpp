@@ -233,5 +233,8 @@ int update_rows_override();
 // FKC_UPDATE_SCAN=0|1: sort-free loop update off / on where it can run;
 // -1 = auto.
 int update_scan_override();
+// FKC_SCAN_WGS=n (1..65536): size the sort-free update's grid to about n
+// workgroups instead of one per CU; 0 = auto.
+int scan_wgs_override();
 
 }  // namespace fkc

@@ -49,7 +49,6 @@
 #include "fkc_internal.hpp"
 
 #include <limits.h>
-#include <cstdlib>
 
 #include <type_traits>
 
@@ -1388,12 +1387,9 @@ int launch_scan_dt(const void* x, const int32_t* ids, const UpdateBufs& w,
 // Labels per workgroup of update_scan: the row's K labels spread so that
 // the launch has about one workgroup per compute unit.
 int64_t scan_kpw(int64_t B, int64_t K) {
-  if (const char* e = std::getenv("FKC_SCAN_WGS")) {
-    const int64_t w = std::atoll(e);
-    if (w > 0) return (B * K + w - 1) / w;
-  }
-  const int64_t cus = device_shape().cus;
-  return (B * K + cus - 1) / cus;
+  const int64_t o = scan_wgs_override();
+  const int64_t w = o > 0 ? o : device_shape().cus;
+  return (B * K + w - 1) / w;
 }
 
 }  // namespace
