@@ -815,34 +815,31 @@ update_merge_kernel(const float* __restrict__ part,
 // With N <= SCAN_NMAX points per row the loop replaces its three launches
 // after the assign (label sort, update_runs, update_merge) by one.  Each
 // workgroup owns `kpw` consecutive labels of one batch row.  It reads the
-// whole row of labels into registers (256-label chunks in index order
-// across its waves), counting the labels below its first one and, per
-// chunk, each of its own by ballots; an exclusive prefix over the chunks
-// (one wave per owned label) then gives every owned row its sorted
-// position: the stable sort's order is label-major, index-minor, so a
-// workgroup can place its own rows without sorting anything else.  Each
-// owned row writes its point index at its sorted position in LDS (a window
-// of SCAN_CAP positions at a time).  From there the sums follow the sort
-// path's units and order bit for bit: sorted positions are cut into units
-// of `ur` rows (choose_ur), each piece of a run inside one unit is summed
-// row by row in sorted order from zero, a run inside one unit is finalized
-// at once, and a longer run
+// whole row of labels into registers, counting the labels below its first
+// one (the start of its range of sorted positions), and sets bit i of
+// owned label j's bitmap for each owned point i.  The stable sort's order
+// is label-major, index-minor, so the set bits of the concatenated bitmaps
+// are its rows in sorted order: an exclusive scan of popcounts gives every
+// owned row its sorted position without sorting anything else, and the row's
+// point index is written to LDS there (a window of SCAN_CAP positions at a
+// time).  From there the sums follow the sort path's units and order bit
+// for bit: sorted positions are cut into units of `ur` rows (choose_ur),
+// each piece of a run inside one unit is summed row by row in sorted order
+// from zero, a run inside one unit is finalized at once, and a longer run
 // keeps its tail partial (first unit) and head partials (later units) in
 // the update workspace, then sums full 64-unit blocks and the run itself by
 // wave_ordered_sum in update_merge's item order (tail, heads of the start
 // block, block partials, heads of the end block), so the centroids, c_sq
 // and shift equal those of label_sort + update_runs + update_merge.
-// Every workgroup reads the whole row of labels, so the plan (update_scan_ok)
-// takes this route only for short rows and few labels per workgroup; a row
-// whose rows crowd into a few labels makes their owners sum them alone.
-constexpr int SCAN_NMAX = 32768;   // labels of a row (held in registers)
+// Every workgroup reads the whole row of labels and a label's rows are
+// summed by its owner alone, so the route serves short rows only.
+constexpr int SCAN_NMAX = 32768;   // labels of a row, at most
 constexpr int SCAN_KPW = 16;       // labels owned per workgroup, at most
 constexpr int SCAN_CAP = 16384;    // sorted positions per placement window
 constexpr int SCAN_T = 1024;       // threads per workgroup (16 waves)
 constexpr int SCAN_W = SCAN_T / 64;
 constexpr int SCAN_UMAX = SCAN_NMAX / (4 * SCAN_T);  // label quads per thread
-constexpr int SCAN_CH = SCAN_UMAX * SCAN_W;          // 256-label chunks, at most
-constexpr int SCAN_LIST = 1024;  // owned rows ranked in a list, at most
+constexpr int SCAN_BM = SCAN_KPW * SCAN_NMAX / 32;   // bitmap words (64 KB)
 
 // SCAN_U: label quads per thread (N <= 4 * SCAN_T * SCAN_U).
 template <int DT, int VEC, int NI, int SCAN_U>
@@ -858,14 +855,11 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
   using R = typename RC::T;
   __shared__ uint16_t s_perm[SCAN_CAP];
   __shared__ float s_row[SCAN_W][FIN_DMAX];
-  // Per 256-label chunk (u, wave) and owned label j: its rows in the chunk,
-  // then their place among the label's rows (exclusive prefix over chunks).
-  __shared__ int s_tab[SCAN_CH][SCAN_KPW];
-  __shared__ __attribute__((aligned(16))) int s_list[SCAN_LIST];
-  __shared__ int s_cnt[SCAN_KPW];
+  // Bit i of word w of label j's bitmap (words j * wpl .. j * wpl + wpl - 1)
+  // is set when point 32 w + i has label k0 + j.
+  __shared__ uint32_t s_bm[SCAN_BM];
   __shared__ int s_off[SCAN_KPW + 1];
   __shared__ int s_red[SCAN_W];
-  __shared__ int s_n;
   if (loop_done(ctrl)) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -876,16 +870,13 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
   const T* xb = x + (size_t)b * N * D;
   float* partb = part + (size_t)b * nunits * 2 * D;
   float* bpartb = bpart + (size_t)b * nblocks * D;
-
-  for (int i = tid; i < SCAN_CH * SCAN_KPW; i += SCAN_T) (&s_tab[0][0])[i] = 0;
-  if (tid < SCAN_KPW) s_cnt[tid] = 0;
-  if (tid == 0) s_n = 0;
+  const int wpl = (N + 31) / 32;  // bitmap words per owned label
+  const int nbw = nk * wpl;       // <= SCAN_BM (plan)
+  for (int i = tid; i < nbw; i += SCAN_T) s_bm[i] = 0u;
 
   // 1. The row's labels stay in registers: thread t holds labels
-  // 4 (t + SCAN_T u) + c, u < SCAN_U, c < 4, so for each u the workgroup
-  // covers SCAN_T * 4 consecutive labels in (wave, lane, c) order and the
-  // chunks (u, wave) of 256 labels run in index order.  All loads are in
-  // flight before any is used; -1 past N.
+  // 4 (t + SCAN_T u) + c, u < SCAN_U, c < 4.  All loads are in flight
+  // before any is used; -1 past N.
   int lab[SCAN_U][4];
 #pragma unroll
   for (int u = 0; u < SCAN_U; ++u) {
@@ -908,6 +899,56 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
     for (int c = 0; c < 4; ++c) below += (lab[u][c] >= 0 && lab[u][c] < k0) ? 1 : 0;
   below = wave_sum_i(below);
   if (lane == 0) s_red[wave] = below;
+  __syncthreads();  // bitmaps cleared, s_red written
+  int S0 = 0;
+#pragma unroll
+  for (int w = 0; w < SCAN_W; ++w) S0 += s_red[w];
+
+  // 2. Each owned row sets its bit.
+#pragma unroll
+  for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const unsigned j = (unsigned)(lab[u][c] - k0);
+      if (j < (unsigned)nk) {
+        const int i = 4 * (tid + SCAN_T * u) + c;
+        atomicOr(&s_bm[j * wpl + (i >> 5)], 1u << (i & 31));
+      }
+    }
+  __syncthreads();
+
+  // 3. In label-major, index-minor order (the stable sort's order) the set
+  // bits of the concatenated bitmaps are the owned rows, so a row's sorted
+  // position is S0 plus the set bits before it.  Thread t takes words
+  // t * wpt .. t * wpt + wpt - 1; an exclusive scan of the threads' counts
+  // gives each thread its first position.
+  const int wpt = (nbw + SCAN_T - 1) / SCAN_T;  // <= SCAN_BM / SCAN_T
+  const int w_lo = min(tid * wpt, nbw), w_hi = min(w_lo + wpt, nbw);
+  int mine = 0;
+  for (int w = w_lo; w < w_hi; ++w) mine += __builtin_popcount(s_bm[w]);
+  int incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  __syncthreads();  // s_red (S0's inputs) read by every thread
+  if (lane == 63) s_red[wave] = incl;
+  __syncthreads();
+  int first = S0 + incl - mine;
+  for (int w = 0; w < wave; ++w) first += s_red[w];
+  // A label's first position: the thread holding its first word.
+  {
+    int p = first;
+    for (int w = w_lo; w < w_hi; ++w) {
+      if (w % wpl == 0) s_off[w / wpl] = p;
+      p += __builtin_popcount(s_bm[w]);
+    }
+    if (tid == SCAN_T - 1) s_off[nk] = p;
+  }
+  __syncthreads();
+  const int S1 = s_off[nk];
+  if (S1 == S0) return;  // every owned label is empty: its centroid stands
 
   int col[NI];
   bool cok[NI];
@@ -932,30 +973,61 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
     wave_lds_sync();
   };
 
-  // Sum the pieces of owned runs in sorted positions [W0, W1) (W0 a unit
-  // boundary, s_perm holding their point indices): each unit of the window,
-  // each owned run in it; units go to the waves in turn.  A run inside one
+  // 4. Windows of SCAN_CAP sorted positions, starting at a unit boundary:
+  // each thread writes the point index of each of its set bits whose
+  // position falls in the window, then the window's pieces (a run's rows
+  // inside one unit) are summed, spread over the waves.  A run inside one
   // unit is finalized at once; a longer run's pieces go to the workspace.
-  auto pieces = [&](int W0, int W1) {
-    const int S0 = s_off[0];
-    for (int u = W0 / ur + wave; u * ur < W1; u += SCAN_W) {
-      const int pa = max(u * ur, S0), pb = min((u + 1) * ur, W1);
-      for (int j = 0; j < nk; ++j) {
+  for (int W0 = S0 / ur * ur; W0 < S1; W0 += SCAN_CAP) {
+    const int W1 = min(W0 + SCAN_CAP, S1);
+    if (first < W1) {
+      int p = first;
+      for (int w = w_lo; w < w_hi && p < W1; ++w) {
+        uint32_t m = s_bm[w];
+        const int i0 = (w % wpl) * 32;
+        while (m != 0u) {
+          const int bit = __builtin_ctz(m);
+          m &= m - 1u;
+          if (p >= W0 && p < W1) s_perm[p - W0] = (uint16_t)(i0 + bit);
+          ++p;
+        }
+      }
+    }
+    __syncthreads();
+    // Pieces in label-major order, (label j, unit u) for the units of
+    // label j's rows inside the window; piece q goes to wave q % SCAN_W.
+    const int uw0 = W0 / ur, uw1 = (W1 - 1) / ur;  // the window's units
+    for (int q = wave;; q += SCAN_W) {
+      int j = 0, u = 0, qq = q;
+      for (; j < nk; ++j) {
         const int s = s_off[j], e = s_off[j + 1];
-        const int a = max(pa, s), z = min(pb, e);
-        if (a >= z) continue;
+        if (s == e) continue;
+        const int lo = max(s / ur, uw0), hi = min((e - 1) / ur, uw1);
+        const int np = hi >= lo ? hi - lo + 1 : 0;
+        if (qq < np) {
+          u = lo + qq;
+          break;
+        }
+        qq -= np;
+      }
+      if (j >= nk) break;
+      {
+        const int s = s_off[j], e = s_off[j + 1];
+        const int a = max(max(u * ur, s), W0), z = min(min((u + 1) * ur, e), W1);
         Acc acc;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
           for (int v = 0; v < VEC; ++v) acc[i][v] = 0.f;
         for (int r0 = a; r0 < z; r0 += RB) {
+          // The batch's point indices, one per lane in a single LDS read,
+          // then taken lane by lane (no LDS round trip per row); min keeps a
+          // row index inside the batch row whatever LDS holds.
+          const int lidx = min((int)s_perm[min(r0 + lane, z - 1) - W0], N - 1);
           R raw[RB][NI];
 #pragma unroll
           for (int jj = 0; jj < RB; ++jj) {
-            const int r = min(r0 + jj, z - 1);
-            // (min: a row index stays inside the batch row whatever LDS holds)
-            const int idx = min(__builtin_amdgcn_readfirstlane((int)s_perm[r - W0]), N - 1);
+            const int idx = __builtin_amdgcn_readlane(lidx, jj);
             const T* row = xb + (size_t)idx * D;
 #pragma unroll
             for (int i = 0; i < NI; ++i) raw[jj][i] = RC::load(row + lcol[i]);
@@ -986,184 +1058,9 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
       }
     }
     __syncthreads();
-  };
-
-  __syncthreads();  // s_tab, s_cnt, s_n cleared; s_red written
-  int S0 = 0;
-#pragma unroll
-  for (int w = 0; w < SCAN_W; ++w) S0 += s_red[w];
-  const int W0 = S0 / ur * ur;
-
-  // 2. The owned rows into a list, key (j << 15) | index: each lane counts
-  // its own, a wave prefix gives its slots and one LDS atomic per wave the
-  // wave's base (the list's order does not matter: it is ranked next).
-  int mine = 0;
-#pragma unroll
-  for (int u = 0; u < SCAN_U; ++u)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) mine += (unsigned)(lab[u][c] - k0) < (unsigned)nk ? 1 : 0;
-  int incl = mine;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += y;
-  }
-  const int wtot = __shfl(incl, 63, 64);
-  if (wtot > 0) {  // wave-uniform
-    int base = 0;
-    if (lane == 0) base = atomicAdd(&s_n, wtot);
-    int slot = __builtin_amdgcn_readfirstlane(base) + incl - mine;
-#pragma unroll
-    for (int u = 0; u < SCAN_U; ++u)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const unsigned j = (unsigned)(lab[u][c] - k0);
-        if (j < (unsigned)nk) {
-          if (slot < SCAN_LIST)
-            s_list[slot] = (int)(j << 15) | (4 * (tid + SCAN_T * u) + c);
-          ++slot;
-        }
-      }
-  }
-  __syncthreads();
-  const int M = s_n;
-  if (M == 0) return;  // every owned label is empty: its centroid stands
-
-  if (M <= SCAN_LIST) {
-    // 3a. A row's place among the owned rows is the number of smaller keys
-    // (keys are distinct); its sorted position is S0 plus that.  The list
-    // is read four keys at a time (every lane the same words: broadcasts).
-    const int4* l4 = reinterpret_cast<const int4*>(s_list);
-    for (int e = tid; e < M; e += SCAN_T) {
-      const int key = s_list[e];
-      int r = 0;
-      const int m4 = M / 4;
-      int f = 0;
-      for (; f + 8 <= m4; f += 8) {  // eight reads in flight
-        int4 q[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = l4[f + i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          r += (q[i].x < key) + (q[i].y < key) + (q[i].z < key) + (q[i].w < key);
-      }
-      for (; f < m4; ++f) {
-        const int4 q = l4[f];
-        r += (q.x < key) + (q.y < key) + (q.z < key) + (q.w < key);
-      }
-      for (int g = 4 * m4; g < M; ++g) r += s_list[g] < key;
-      s_perm[S0 + r - W0] = (uint16_t)(key & 0x7fff);
-      atomicAdd(&s_cnt[key >> 15], 1);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int base = S0;
-      for (int j = 0; j < nk; ++j) {
-        s_off[j] = base;
-        base += s_cnt[j];
-      }
-      s_off[nk] = base;
-    }
-    __syncthreads();
-    pieces(W0, S0 + M);
-  } else {
-    // 3b. Too many owned rows for the list: walk the chunks in index order.
-    // Visit the owned labels of chunk (u, this wave) one value at a time
-    // (only the values present): fn(j, pre, tot, mine) with pre the rows of
-    // label k0 + j in lower lanes, tot the chunk's, mine[c] this lane's.
-    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    auto for_owned = [&](int u, auto fn) {
-      bool pend[4];
-      bool any = false;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        pend[c] = (unsigned)(lab[u][c] - k0) < (unsigned)nk;
-        any |= pend[c];
-      }
-      for (;;) {
-        const uint64_t m = __builtin_amdgcn_ballot_w64(any);
-        if (m == 0) break;
-        const int first = pend[0] ? lab[u][0]
-                          : pend[1] ? lab[u][1]
-                          : pend[2] ? lab[u][2] : lab[u][3];
-        const int v = __builtin_amdgcn_readlane(first, (int)__builtin_ctzll(m));
-        bool mine[4];
-        int cj = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          mine[c] = pend[c] && lab[u][c] == v;
-          cj += mine[c] ? 1 : 0;
-          pend[c] = pend[c] && !mine[c];
-        }
-        any = pend[0] || pend[1] || pend[2] || pend[3];
-        const uint64_t m0 = __builtin_amdgcn_ballot_w64(cj & 1);
-        const uint64_t m1 = __builtin_amdgcn_ballot_w64(cj & 2);
-        const uint64_t m2 = __builtin_amdgcn_ballot_w64(cj & 4);
-        const int pre = __builtin_popcountll(m0 & lt) +
-                        2 * __builtin_popcountll(m1 & lt) +
-                        4 * __builtin_popcountll(m2 & lt);
-        const int tot = __builtin_popcountll(m0) + 2 * __builtin_popcountll(m1) +
-                        4 * __builtin_popcountll(m2);
-        fn(v - k0, pre, tot, mine);
-      }
-    };
-#pragma unroll
-    for (int u = 0; u < SCAN_U; ++u)
-      for_owned(u, [&](int j, int, int tot, const bool*) {
-        if (lane == 0) s_tab[u * SCAN_W + wave][j] = tot;
-      });
-    __syncthreads();
-    // Wave j turns label k0 + j's chunk counts into exclusive prefixes
-    // (two chunks per lane) and its total.
-    if (wave < nk) {
-      const int j = wave;
-      const int e0 = s_tab[2 * lane][j], e1 = s_tab[2 * lane + 1][j];
-      int x0 = e0 + e1;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x0, d, 64);
-        if (lane >= d) x0 += y;
-      }
-      const int excl = x0 - e0 - e1;
-      s_tab[2 * lane][j] = excl;
-      s_tab[2 * lane + 1][j] = excl + e0;
-      if (lane == 63) s_cnt[j] = x0;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int base = S0;
-      for (int j = 0; j < nk; ++j) {
-        s_off[j] = base;
-        base += s_cnt[j];
-      }
-      s_off[nk] = base;
-    }
-    __syncthreads();
-    const int S1 = s_off[nk];
-    // Windows of SCAN_CAP sorted positions, starting at a unit boundary: a
-    // row's sorted position is its label's first position, plus its
-    // label's rows in earlier chunks, in lower lanes of its chunk, and in
-    // lower c of its lane.
-    for (int w0 = W0; w0 < S1; w0 += SCAN_CAP) {
-      const int w1 = min(w0 + SCAN_CAP, S1);
-#pragma unroll
-      for (int u = 0; u < SCAN_U; ++u)
-        for_owned(u, [&](int j, int pre, int, const bool* mine) {
-          int p = s_off[j] + s_tab[u * SCAN_W + wave][j] + pre;
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (mine[c]) {
-              if (p >= w0 && p < w1)
-                s_perm[p - w0] = (uint16_t)(4 * (tid + SCAN_T * u) + c);
-              ++p;
-            }
-        });
-      __syncthreads();
-      pieces(w0, w1);
-    }
   }
 
-  // 4. Runs over several units: full 64-unit blocks first (update_runs'
+  // 5. Runs over several units: full 64-unit blocks first (update_runs'
   // block sums), then each run in update_merge's item order.
   auto run_items = [&](int s, int e, int& n1, int& beta0, int& nblk, int& v3,
                        int& n3) {
@@ -1184,22 +1081,30 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
     v3 = be * UB;
     n3 = ue - v3 + 1;
   };
-  for (int j = wave; j < nk; j += SCAN_W) {
-    const int s = s_off[j], e = s_off[j + 1];
-    if (e - s == 0 || s / ur == (e - 1) / ur) continue;
-    int n1, beta0, nblk, v3, n3;
-    run_items(s, e, n1, beta0, nblk, v3, n3);
-    for (int q = 0; q < nblk; ++q) {
-      const int beta = beta0 + q;
-      auto row = [&](int i) {
-        return partb + ((size_t)(beta * UB + i) * 2 + 0) * D;
-      };
-      float* dst = bpartb + (size_t)beta * D;
-      if (D % 4 == 0)
-        wave_ordered_sum<4>(nullptr, UB, 0, D, row, dst, 0, lane);
-      else
-        wave_ordered_sum<1>(nullptr, UB, 0, D, row, dst, 0, lane);
+  // The full blocks of all owned runs, in label order, spread over the
+  // waves (a crowded label's blocks are summed in parallel).
+  for (int q = wave;; q += SCAN_W) {
+    int beta = -1, qq = q;
+    for (int j = 0; j < nk; ++j) {
+      const int s = s_off[j], e = s_off[j + 1];
+      if (e - s == 0 || s / ur == (e - 1) / ur) continue;
+      int n1, beta0, nblk, v3, n3;
+      run_items(s, e, n1, beta0, nblk, v3, n3);
+      if (qq < nblk) {
+        beta = beta0 + qq;
+        break;
+      }
+      qq -= nblk;
     }
+    if (beta < 0) break;
+    auto row = [&](int i) {
+      return partb + ((size_t)(beta * UB + i) * 2 + 0) * D;
+    };
+    float* dst = bpartb + (size_t)beta * D;
+    if (D % 4 == 0)
+      wave_ordered_sum<4>(nullptr, UB, 0, D, row, dst, 0, lane);
+    else
+      wave_ordered_sum<1>(nullptr, UB, 0, D, row, dst, 0, lane);
   }
   __syncthreads();
   for (int j = wave; j < nk; j += SCAN_W) {
@@ -1471,18 +1376,17 @@ bool update_scan_ok(int64_t B, int64_t N, int64_t K, int64_t D) {
   if (D < 1 || D > FIN_DMAX || D > (int64_t)64 * runs_vec(D) * runs_ni(D))
     return false;
   if (scan_kpw(B, K) > SCAN_KPW) return false;
-  // Taken on its own for rows of at most 8192 points, where it measured
-  // faster than the three launches it replaces (loop time per iteration,
-  // same box, random rows, scan vs sort: (1, 2048, 64, 128) f16 14.2 vs
-  // 20.9 us, c1's (1, 4096, 64, 128) f32 20.0 vs 25.0, (1, 4096, 256, 128)
-  // 16.9 vs 25.2, (1, 8192, 256, 128) 17.7 vs 25.8, (1, 8192, 1024, 64)
-  // bf16 23.8 vs 33.9, (4, 8192, 128, 64) 18.6 vs 21.7).  Every workgroup
-  // walks its whole row of labels and each label's rows are summed by their
-  // owner alone, so longer rows gain less and lose where labels crowd: c2's
-  // (1, 32768, 256, 128), whose largest cluster holds 550 rows, 33.7 vs
-  // 29.7 us (random rows of that shape: 24.6 vs 27.8); (1, 16384, 64, 32)
-  // 21.0 vs 20.2.
-  return o == 1 || (N <= 8192 && N <= 256 * K);
+  // Taken on its own for every row it can hold, where it measured faster
+  // than the three launches it replaces (loop time per iteration, same box,
+  // scan vs sort: c1's (1, 4096, 64, 128) f32 18.8 vs 24.8 us, c2's
+  // (1, 32768, 256, 128) f16 mixture 27.1 vs 30.2, random rows
+  // (1, 2048, 64, 128) 14.2 vs 20.6, (1, 8192, 256, 128) 17.4 vs 25.7,
+  // (1, 8192, 1024, 64) bf16 21.9 vs 33.5, (4, 8192, 128, 64) 16.4 vs
+  // 21.6, (1, 16384, 64, 32) 17.1 vs 20.0).  A label's rows are summed by
+  // its owner's 16 waves alone, so rows crowded into one label cost more
+  // than the sort path spreading them over the chip: half or 95% of 32768
+  // points on one spot, 56-77 vs 34-41 us; at 16384 points 25.7 vs 30.8.
+  return o == 1 || N <= 256 * K;
 }
 
 int launch_update_scan(const void* x, const int32_t* ids, int64_t B,
