@@ -364,7 +364,7 @@ def _report(configs) -> int:
         print(json.dumps(row), flush=True)
     print("| config | (B, N, K, D) dtype | assign ms | assign TFLOP/s | ms/iter steady | "
           "ms/iter one call | ideal ms/iter | ideal/measured | reference ms/iter (RTX 4090) | "
-          "CPU oracle ms/iter (threads) |")
+          "CPU ms/iter (threads) |")
     print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|")
     for r in rows:
         print(f"| {r['config']} | ({r['B']}, {r['N']}, {r['K']}, {r['D']}) {r['dtype']} | "
