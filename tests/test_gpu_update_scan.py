@@ -57,6 +57,9 @@ def _same(a, b, what):
     (16, 2048, 200, 16, "f32"),      # thirteen labels per workgroup
     (1, 1, 1, 16, "f16"),
     (2, 70, 64, 8, "bf16"),          # most clusters empty
+    (1, 8192, 300, 64, "f16"),       # the largest row of two label quads per thread
+    (1, 8193, 300, 64, "f16"),       # the smallest of eight
+    (2, 32768, 256, 128, "bf16"),    # the largest row, batched
 ])
 def test_scan_update_equals_sort_path(monkeypatch, B, N, K, D, dtype):
     from flash_kmeans_cuda import batch_kmeans_Euclid
