@@ -1370,8 +1370,25 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
     // not two: at N = 65536, K = 8192 three slices took 0.117 ms, four
     // 0.122, none 0.121; at N = 32768, K = 16384 six 0.123, three 0.138,
     // none 0.220; at N = 131072, K = 4096 two slices (two rounds) lost 6%.
-    S = std::min<int64_t>(3 * device_shape().cus / tiles,
-                          K / FKC_SLICE_MIN_ROWS);
+    // Where whole slices of at most 4096 rows also fill one round of the
+    // kept-score variant's workgroups (2 per CU) as fully, that round runs
+    // with no re-score (same-box assign times, kept scores on 2 x CUs /
+    // tiles slices against the re-score on 3 x CUs / tiles: N = 65536,
+    // K = 8192 0.112 vs 0.117 ms; N = 32768, K = 16384 0.112 vs 0.119;
+    // N = 16384, K = 32768 0.113 vs 0.122; at 8192-row slices it lost,
+    // 0.215 vs 0.209, and at N = 49152 (a three-quarter round) 0.096 vs
+    // 0.088).
+    const int64_t cus = device_shape().cus;
+    const int64_t s3 = std::min<int64_t>(3 * cus / tiles, K / FKC_SLICE_MIN_ROWS);
+    const int64_t s2 = std::min<int64_t>(2 * cus / tiles, K / FKC_SLICE_MIN_ROWS);
+    S = s3;
+    if (s2 >= 2) {
+      const int64_t span2 = ((K + s2 - 1) / s2 + 127) / 128 * 128;
+      if (span2 <= 4096 &&
+          round_fill(tiles * s2, 2 * cus) >=
+              round_fill(tiles * std::max<int64_t>(s3, 1), 3 * cus))
+        S = s2;
+    }
     if (S <= 1) return p;
   } else if (S == 0) {
     const int64_t want = fill_wgs(pt, p.ds2, p.exact);

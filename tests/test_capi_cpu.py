@@ -156,7 +156,9 @@ def test_assign_slice_plan(monkeypatch):
     the four-tile workgroups of all slices fill one round of 768 (3 per CU)
     with slices of >= 2048 rows: none for the benchmark shape (c5, 1024
     eight-tile workgroups) or c3 (512 four-tile workgroups, slices would be
-    1024 rows), 3 for c5's one-GPU share of eight (256 workgroups).  Other
+    1024 rows); where slices of <= 4096 rows fill one round of 512 (the
+    kept-score variant, 2 per CU) as fully, those: 2 for c5's one-GPU share
+    of eight (256 workgroups), 4 for (32768, 16384).  Other
     widths slice only when no unsliced grid fills the chip: none for c4
     (2048 workgroups).  None for K <= 512 (exact in-loop index), the fp32
     route, or slices shorter than 2048 rows.  FKC_KSPLIT forces a count."""
@@ -167,8 +169,9 @@ def test_assign_slice_plan(monkeypatch):
     half = lambda n: (n * 4 + 255) // 256 * 256
     assert f(1, 524288, 8192, 128, 1) == 0
     assert f(1, 131072, 2048, 128, 1) == 0
-    assert f(1, 65536, 8192, 128, 2) == 2 * half(3 * 65536)   # 2816-row slices
-    assert f(1, 32768, 16384, 128, 1) == 2 * half(6 * 32768)
+    assert f(1, 65536, 8192, 128, 2) == 2 * half(2 * 65536)   # 4096-row slices
+    assert f(1, 32768, 16384, 128, 1) == 2 * half(4 * 32768)
+    assert f(1, 49152, 8192, 128, 1) == 2 * half(4 * 49152)   # three-quarter round: re-score
     assert f(1, 32768, 256, 128, 1) == 0
     assert f(8, 65536, 1024, 64, 2) == 0
     assert f(1, 131072, 2048, 128, 0) == 0
