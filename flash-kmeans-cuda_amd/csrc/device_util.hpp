@@ -83,6 +83,21 @@ __device__ inline float row_sum(float v) {
       float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Inclusive scan over the 64 lanes by DPP adds: row_shr 1, 2, 4, 8 scan
+// each 16-lane row, row_bcast:15 adds row 0's total to row 1 and row 2's to
+// row 3, row_bcast:31 adds lane 31 (rows 0 and 1) to rows 2 and 3.  Lanes
+// without a source add the `old` operand, 0.  (A __shfl_up ladder costs an
+// LDS-crossbar round trip per step.)
+__device__ inline int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
 // Number of set bits of `mask` in lanes below the calling lane.
 __device__ inline uint32_t lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(

@@ -205,6 +205,50 @@ __device__ inline void finalize_row(const float* row, int cnt,
   finish_norms(sq, sh, csq, shift, lane);
 }
 
+// A run's unit partials merged and the row finalized in one pass, lane by
+// lane over finalize_row's columns.  part holds the tail (slot 0) and the n
+// heads in item order (slots 1..n), in LDS; each column is summed with
+// wave_ordered_sum's bracketing (four groups, group g adding items g, g+4,
+// ... in order to a zero start, the tail starting group 0, then the groups
+// added in order), so the row gets the bits of wave_ordered_sum followed by
+// finalize_row, without the row buffer or the lane exchanges.
+template <int DT>
+__device__ inline void merge_finalize(const float* part, int n, int cnt,
+                                      typename Elem<DT>::T* crow, float* csq,
+                                      float* shift, int D, int lane) {
+  using E = Elem<DT>;
+  const float fc = (float)cnt;
+  const int vec = row_vec(D);
+  float sq = 0.f, sh = 0.f;
+  for (int c = vec * lane; c < D; c += vec * 64) {
+    for (int v = 0; v < vec; ++v) {
+      const int d = c + v;
+      const float* it = part + D + d;
+      float g0 = part[d], g1 = 0.f, g2 = 0.f, g3 = 0.f;
+      int i = 0;
+      for (; i + 4 <= n; i += 4) {
+        g0 += it[i * D];
+        g1 += it[(i + 1) * D];
+        g2 += it[(i + 2) * D];
+        g3 += it[(i + 3) * D];
+      }
+      if (i < n) g0 += it[i * D];
+      if (i + 1 < n) g1 += it[(i + 1) * D];
+      if (i + 2 < n) g2 += it[(i + 2) * D];
+      const float tot = ((g0 + g1) + g2) + g3;
+      const typename E::T nv = E::store(tot / fc);
+      const float nf = E::load(nv);
+      if (shift != nullptr) {
+        const float df = nf - E::load(crow[d]);
+        sh = fmaf(df, df, sh);
+      }
+      crow[d] = nv;
+      sq = fmaf(nf, nf, sq);
+    }
+  }
+  finish_norms(sq, sh, csq, shift, lane);
+}
+
 // Wave-cooperative ordered sum of partial rows (D fp32 each):
 //   out[c] = first[c] + row(0)[c] + ... + row(n-1)[c]   (first may be null)
 // for the columns c in [c_lo, c_hi).  The wave splits into G lane groups;
@@ -833,6 +877,11 @@ update_merge_kernel(const float* __restrict__ part,
 // and shift equal those of label_sort + update_runs + update_merge.
 // Every workgroup reads the whole row of labels and a label's rows are
 // summed by its owner alone, so the route serves short rows only.
+// FKC_SCAN_ONE=0 (compile time, for A/B builds) sends one-label
+// workgroups through the bitmap placement too.
+#ifndef FKC_SCAN_ONE
+#define FKC_SCAN_ONE 1
+#endif
 constexpr int SCAN_NMAX = 32768;   // labels of a row, at most
 constexpr int SCAN_KPW = 16;       // labels owned per workgroup, at most
 constexpr int SCAN_CAP = 16384;    // sorted positions per placement window
@@ -841,8 +890,17 @@ constexpr int SCAN_W = SCAN_T / 64;
 constexpr int SCAN_UMAX = SCAN_NMAX / (4 * SCAN_T);  // label quads per thread
 constexpr int SCAN_BM = SCAN_KPW * SCAN_NMAX / 32;   // bitmap words (64 KB)
 
-// SCAN_U: label quads per thread (N <= 4 * SCAN_T * SCAN_U).
-template <int DT, int VEC, int NI, int SCAN_U>
+// SCAN_U: label quads per thread (N <= 4 * SCAN_T * SCAN_U).  ONE: the
+// workgroup owns one label (kpw == 1).  Its rows are then placed without
+// bitmaps: for each 256-point chunk (one wave's labels of one quad index u)
+// the wave takes a ballot per quad slot, the chunks' match counts are
+// scanned once in chunk order (which is index order), and a row's sorted
+// position is its chunk's offset plus the matches in lower lanes (mbcnt)
+// and in its own lane's lower slots.  The bitmap's LDS then holds the
+// run's unit partials when they fit (a run over a few units), so the merge
+// reads them from LDS instead of the workspace.  Positions, pieces and
+// summation order are those of the bitmap path, so the bits are the same.
+template <int DT, int VEC, int NI, int SCAN_U, bool ONE>
 __global__ void __launch_bounds__(SCAN_T)
 update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
                    const int32_t* __restrict__ ids, float* __restrict__ part,
@@ -853,101 +911,173 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
   using T = typename Elem<DT>::T;
   using RC = RawCols<DT, VEC>;
   using R = typename RC::T;
-  __shared__ uint16_t s_perm[SCAN_CAP];
+  // Sorted positions of the current window; ONE: 128 more entries give
+  // each lane a slot of its own for the stores of rows it does not place.
+  __shared__ uint16_t s_perm[SCAN_CAP + (ONE ? 128 : 0)];
   __shared__ float s_row[SCAN_W][FIN_DMAX];
   // Bit i of word w of label j's bitmap (words j * wpl .. j * wpl + wpl - 1)
-  // is set when point 32 w + i has label k0 + j.
-  __shared__ uint32_t s_bm[SCAN_BM];
+  // is set when point 32 w + i has label k0 + j.  ONE: unit partials.
+  __shared__ __attribute__((aligned(16))) uint32_t s_bm[SCAN_BM];
   __shared__ int s_off[SCAN_KPW + 1];
   __shared__ int s_red[SCAN_W];
+  __shared__ int s_cnt[ONE ? SCAN_W * SCAN_U : 1];  // ONE: matches per chunk
   if (loop_done(ctrl)) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.y;
   const int k0 = blockIdx.x * kpw;
-  const int nk = min(kpw, K - k0);  // >= 1: the grid covers K exactly
+  const int nk = ONE ? 1 : min(kpw, K - k0);  // >= 1: the grid covers K exactly
   const int32_t* ib = ids + (size_t)b * N;
   const T* xb = x + (size_t)b * N * D;
   float* partb = part + (size_t)b * nunits * 2 * D;
   float* bpartb = bpart + (size_t)b * nblocks * D;
   const int wpl = (N + 31) / 32;  // bitmap words per owned label
   const int nbw = nk * wpl;       // <= SCAN_BM (plan)
-  for (int i = tid; i < nbw; i += SCAN_T) s_bm[i] = 0u;
+  if constexpr (!ONE)
+    for (int i = tid; i < nbw; i += SCAN_T) s_bm[i] = 0u;
 
   // 1. The row's labels stay in registers: thread t holds labels
   // 4 (t + SCAN_T u) + c, u < SCAN_U, c < 4.  All loads are in flight
   // before any is used; -1 past N.
+  // Branch-free: indices are clamped into the row and labels past N read
+  // as INT_MAX (never owned, never below k0).  vec4 implies N % 4 == 0, so
+  // a quad is wholly inside the row or wholly past it.
   int lab[SCAN_U][4];
+  if (vec4) {
 #pragma unroll
-  for (int u = 0; u < SCAN_U; ++u) {
-    const int i0 = 4 * (tid + SCAN_T * u);
-    if (vec4 && i0 + 3 < N) {
-      const int4 v = *reinterpret_cast<const int4*>(ib + i0);
-      lab[u][0] = v.x;
-      lab[u][1] = v.y;
-      lab[u][2] = v.z;
-      lab[u][3] = v.w;
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) lab[u][c] = i0 + c < N ? ib[i0 + c] : -1;
+    for (int u = 0; u < SCAN_U; ++u) {
+      const int i0 = 4 * (tid + SCAN_T * u);
+      const int4 v = *reinterpret_cast<const int4*>(ib + min(i0, N - 4));
+      const bool in = i0 < N;
+      lab[u][0] = in ? v.x : INT_MAX;
+      lab[u][1] = in ? v.y : INT_MAX;
+      lab[u][2] = in ? v.z : INT_MAX;
+      lab[u][3] = in ? v.w : INT_MAX;
     }
+  } else {
+#pragma unroll
+    for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int i = 4 * (tid + SCAN_T * u) + c;
+        const int l = ib[min(i, N - 1)];
+        lab[u][c] = i < N ? l : INT_MAX;
+      }
   }
   int below = 0;
 #pragma unroll
   for (int u = 0; u < SCAN_U; ++u)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) below += (lab[u][c] >= 0 && lab[u][c] < k0) ? 1 : 0;
+    for (int c = 0; c < 4; ++c) below += (unsigned)lab[u][c] < (unsigned)k0 ? 1 : 0;
   below = wave_sum_i(below);
   if (lane == 0) s_red[wave] = below;
-  __syncthreads();  // bitmaps cleared, s_red written
+  // ONE: chunk (u, wave) holds points 4 (SCAN_T u + 64 wave) .. + 255, so
+  // chunk q = SCAN_W u + wave runs in index order; rk[u] is this lane's
+  // first match's rank inside its chunk (the matches of lower lanes).  The
+  // lanes' match counts of three quads share a word (10-bit fields: a
+  // chunk holds at most 256), so one DPP scan ranks three chunks.
+  // own: bit 4u + c set when label (u, c) is the owned one.
+  int rk[ONE ? SCAN_U : 1];
+  uint32_t own = 0u;
+  if constexpr (ONE) {
+#pragma unroll
+    for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) own |= (lab[u][c] == k0 ? 1u : 0u) << (4 * u + c);
+    constexpr int NW = (SCAN_U + 2) / 3;
+    int pk[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) pk[w] = 0;
+#pragma unroll
+    for (int u = 0; u < SCAN_U; ++u)
+      pk[u / 3] += __builtin_popcount((own >> (4 * u)) & 15u) << (10 * (u % 3));
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int inc = wave_incl_scan(pk[w]);
+      const int exc = inc - pk[w];
+      const int tot = __builtin_amdgcn_readlane(inc, 63);
+#pragma unroll
+      for (int f = 0; f < 3 && 3 * w + f < SCAN_U; ++f) {
+        const int u = 3 * w + f;
+        rk[u] = (exc >> (10 * f)) & 1023;
+        if (lane == 0) s_cnt[SCAN_W * u + wave] = (tot >> (10 * f)) & 1023;
+      }
+    }
+  }
+  __syncthreads();  // bitmaps cleared, s_red (and s_cnt) written
   int S0 = 0;
 #pragma unroll
   for (int w = 0; w < SCAN_W; ++w) S0 += s_red[w];
 
-  // 2. Each owned row sets its bit.
+  int first = 0, w_lo = 0, w_hi = 0, S1;
+  if constexpr (ONE) {
+    // Exclusive offsets of the SCAN_W * SCAN_U chunks: lane l scans chunks
+    // 2l and 2l + 1 as a pair; chunk q's offset is then the pair offset of
+    // lane q / 2, plus chunk q - 1 when q is odd (q's parity is the wave's).
+    constexpr int NC = SCAN_W * SCAN_U;  // <= 128
+    const int ca = 2 * lane < NC ? s_cnt[2 * lane] : 0;
+    const int cb = 2 * lane + 1 < NC ? s_cnt[2 * lane + 1] : 0;
+    const int inc = wave_incl_scan(ca + cb);
+    const int exc = inc - ca - cb;
 #pragma unroll
-  for (int u = 0; u < SCAN_U; ++u)
+    for (int u = 0; u < SCAN_U; ++u) {
+      const int q = SCAN_W * u + wave;
+      int o = __builtin_amdgcn_readlane(exc, q >> 1);
+      if (q & 1) o += __builtin_amdgcn_readlane(ca, q >> 1);
+      rk[u] += S0 + o;
+    }
+    S1 = S0 + __builtin_amdgcn_readlane(inc, 63);
+    if (tid == 0) {
+      s_off[0] = S0;
+      s_off[1] = S1;
+    }
+  } else {
+    // 2. Each owned row sets its bit.
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const unsigned j = (unsigned)(lab[u][c] - k0);
-      if (j < (unsigned)nk) {
-        const int i = 4 * (tid + SCAN_T * u) + c;
-        atomicOr(&s_bm[j * wpl + (i >> 5)], 1u << (i & 31));
+    for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const unsigned j = (unsigned)(lab[u][c] - k0);
+        if (j < (unsigned)nk) {
+          const int i = 4 * (tid + SCAN_T * u) + c;
+          atomicOr(&s_bm[j * wpl + (i >> 5)], 1u << (i & 31));
+        }
       }
-    }
-  __syncthreads();
+    __syncthreads();
 
-  // 3. In label-major, index-minor order (the stable sort's order) the set
-  // bits of the concatenated bitmaps are the owned rows, so a row's sorted
-  // position is S0 plus the set bits before it.  Thread t takes words
-  // t * wpt .. t * wpt + wpt - 1; an exclusive scan of the threads' counts
-  // gives each thread its first position.
-  const int wpt = (nbw + SCAN_T - 1) / SCAN_T;  // <= SCAN_BM / SCAN_T
-  const int w_lo = min(tid * wpt, nbw), w_hi = min(w_lo + wpt, nbw);
-  int mine = 0;
-  for (int w = w_lo; w < w_hi; ++w) mine += __builtin_popcount(s_bm[w]);
-  int incl = mine;
+    // 3. In label-major, index-minor order (the stable sort's order) the set
+    // bits of the concatenated bitmaps are the owned rows, so a row's sorted
+    // position is S0 plus the set bits before it.  Thread t takes words
+    // t * wpt .. t * wpt + wpt - 1; an exclusive scan of the threads' counts
+    // gives each thread its first position.
+    const int wpt = (nbw + SCAN_T - 1) / SCAN_T;  // <= SCAN_BM / SCAN_T
+    w_lo = min(tid * wpt, nbw);
+    w_hi = min(w_lo + wpt, nbw);
+    int mine = 0;
+    for (int w = w_lo; w < w_hi; ++w) mine += __builtin_popcount(s_bm[w]);
+    int incl = mine;
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += y;
-  }
-  __syncthreads();  // s_red (S0's inputs) read by every thread
-  if (lane == 63) s_red[wave] = incl;
-  __syncthreads();
-  int first = S0 + incl - mine;
-  for (int w = 0; w < wave; ++w) first += s_red[w];
-  // A label's first position: the thread holding its first word.
-  {
-    int p = first;
-    for (int w = w_lo; w < w_hi; ++w) {
-      if (w % wpl == 0) s_off[w / wpl] = p;
-      p += __builtin_popcount(s_bm[w]);
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
     }
-    if (tid == SCAN_T - 1) s_off[nk] = p;
+    __syncthreads();  // s_red (S0's inputs) read by every thread
+    if (lane == 63) s_red[wave] = incl;
+    __syncthreads();
+    first = S0 + incl - mine;
+    for (int w = 0; w < wave; ++w) first += s_red[w];
+    // A label's first position: the thread holding its first word.
+    {
+      int p = first;
+      for (int w = w_lo; w < w_hi; ++w) {
+        if (w % wpl == 0) s_off[w / wpl] = p;
+        p += __builtin_popcount(s_bm[w]);
+      }
+      if (tid == SCAN_T - 1) s_off[nk] = p;
+    }
+    __syncthreads();
+    S1 = s_off[nk];
   }
-  __syncthreads();
-  const int S1 = s_off[nk];
   if (S1 == S0) return;  // every owned label is empty: its centroid stands
 
   int col[NI];
@@ -973,14 +1103,68 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
     wave_lds_sync();
   };
 
+  // The items of a run over several units, in update_merge's order: the
+  // heads of units us+1 .. bend-1 (n1), then nblk full 64-unit blocks from
+  // block beta0 (their block partials), then the heads of units v3 .. ue
+  // (n3); the tail of unit us comes first.
+  auto run_items = [&](int s, int e, int& n1, int& beta0, int& nblk, int& v3,
+                       int& n3) {
+    const int us = s / ur, ue = (e - 1) / ur;
+    const int bend = min((us / UB + 1) * UB, nunits);
+    beta0 = us / UB + 1;
+    nblk = 0;
+    n3 = 0;
+    v3 = 0;
+    if (ue < bend) {
+      n1 = ue - us;
+      return;
+    }
+    n1 = bend - (us + 1);
+    int be = beta0;
+    while ((int64_t)(be + 1) * UB * ur < e) ++be;  // blocks wholly inside
+    nblk = be - beta0;
+    v3 = be * UB;
+    n3 = ue - v3 + 1;
+  };
+  // ONE: a run over 2+ units and no full block keeps its unit partials in
+  // LDS (slot u - us holds unit u's piece: slot 0 the tail, then the heads
+  // in item order) when they fit where the bitmaps would be.
+  float* s_part = reinterpret_cast<float*>(s_bm);
+  bool lds_part = false;
+  if constexpr (ONE) {
+    const int us = S0 / ur, ue = (S1 - 1) / ur;
+    if (us != ue) {
+      int n1, beta0, nblk, v3, n3;
+      run_items(S0, S1, n1, beta0, nblk, v3, n3);
+      lds_part = nblk == 0 && (ue - us + 1) * D <= SCAN_BM;
+    }
+  }
+
   // 4. Windows of SCAN_CAP sorted positions, starting at a unit boundary:
-  // each thread writes the point index of each of its set bits whose
+  // each thread writes the point index of each of its owned rows whose
   // position falls in the window, then the window's pieces (a run's rows
   // inside one unit) are summed, spread over the waves.  A run inside one
-  // unit is finalized at once; a longer run's pieces go to the workspace.
+  // unit is finalized at once; a longer run's pieces go to the workspace
+  // (ONE: to LDS where lds_part).
   for (int W0 = S0 / ur * ur; W0 < S1; W0 += SCAN_CAP) {
     const int W1 = min(W0 + SCAN_CAP, S1);
-    if (first < W1) {
+    if constexpr (ONE) {
+      // One trip per owned row of the lane (owned rows are sparse): its
+      // quad's rank rk[u] picked by selects, plus the owned rows below it
+      // in the same quad; a row outside the window stores into the lane's
+      // own spare entry.
+      const unsigned span = (unsigned)(W1 - W0);
+      for (uint32_t m = own; m != 0u; m &= m - 1u) {
+        const int bit = __builtin_ctz(m);
+        const int u = bit >> 2;
+        int r = rk[0];
+#pragma unroll
+        for (int v = 1; v < SCAN_U; ++v) r = u == v ? rk[v] : r;
+        const int p = r + __builtin_popcount(own & (((1u << bit) - 1u) & (15u << (4 * u)))) - W0;
+        s_perm[(unsigned)p < span ? p : SCAN_CAP + 2 * lane] =
+            (uint16_t)(4 * (tid + SCAN_T * u) + (bit & 3));
+      }
+    } else if (first < W1) {
       int p = first;
       for (int w = w_lo; w < w_hi && p < W1; ++w) {
         uint32_t m = s_bm[w];
@@ -1046,8 +1230,9 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
           }
         }
         const int us = s / ur, ue = (e - 1) / ur;
-        float* dst = us == ue ? s_row[wave]
-                              : partb + ((size_t)u * 2 + (u == us ? 1 : 0)) * D;
+        float* dst = us == ue  ? s_row[wave]
+                     : lds_part ? s_part + (size_t)(u - us) * D
+                                : partb + ((size_t)u * 2 + (u == us ? 1 : 0)) * D;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
           if (cok[i]) {
@@ -1060,27 +1245,20 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
     __syncthreads();
   }
 
-  // 5. Runs over several units: full 64-unit blocks first (update_runs'
-  // block sums), then each run in update_merge's item order.
-  auto run_items = [&](int s, int e, int& n1, int& beta0, int& nblk, int& v3,
-                       int& n3) {
-    const int us = s / ur, ue = (e - 1) / ur;
-    const int bend = min((us / UB + 1) * UB, nunits);
-    beta0 = us / UB + 1;
-    nblk = 0;
-    n3 = 0;
-    v3 = 0;
-    if (ue < bend) {
-      n1 = ue - us;
+  // ONE with the partials in LDS: no blocks, one run; wave 0 merges and
+  // finalizes it.
+  if constexpr (ONE) {
+    if (lds_part) {
+      if (wave == 0)
+        merge_finalize<DT>(s_part, (S1 - 1) / ur - S0 / ur, S1 - S0,
+                           fin.cent + ((size_t)b * K + k0) * D,
+                           fin.c_sq + (size_t)b * K + k0, fin.shift, D, lane);
       return;
     }
-    n1 = bend - (us + 1);
-    int be = beta0;
-    while ((int64_t)(be + 1) * UB * ur < e) ++be;  // blocks wholly inside
-    nblk = be - beta0;
-    v3 = be * UB;
-    n3 = ue - v3 + 1;
-  };
+  }
+
+  // 5. Runs over several units: full 64-unit blocks first (update_runs'
+  // block sums), then each run in update_merge's item order.
   // The full blocks of all owned runs, in label order, spread over the
   // waves (a crowded label's blocks are summed in parallel).
   for (int q = wave;; q += SCAN_W) {
@@ -1255,18 +1433,26 @@ int launch_scan_t(const void* x, const int32_t* ids, const UpdateBufs& w,
   FinArgs<T> fa{static_cast<T*>(f.cent), f.c_sq, f.shift};
   dim3 grid((unsigned)((K + kpw - 1) / kpw), (unsigned)B);
   // Two register budgets for the row's labels: rows up to 8192 hold two
-  // quads per thread, longer ones SCAN_UMAX.
-  if (N <= 8 * SCAN_T)
-    hipLaunchKernelGGL((update_scan_kernel<DT, VEC, NI, 2>), grid, dim3(SCAN_T),
-                       0, s, static_cast<const T*>(x), ids, w.part, w.bpart,
-                       (int)N, (int)K, (int)D, (int)w.nunits, (int)w.nblocks,
-                       choose_ur(B, N), kpw, vec4, fa, ctrl);
-  else
-    hipLaunchKernelGGL((update_scan_kernel<DT, VEC, NI, SCAN_UMAX>), grid,
-                       dim3(SCAN_T), 0, s, static_cast<const T*>(x), ids,
-                       w.part, w.bpart, (int)N, (int)K, (int)D,
-                       (int)w.nunits, (int)w.nblocks, choose_ur(B, N), kpw,
-                       vec4, fa, ctrl);
+  // quads per thread, longer ones SCAN_UMAX; one owned label per workgroup
+  // takes the ballot placement.
+#define FKC_SCAN_LAUNCH(U, ONE_)                                              \
+  hipLaunchKernelGGL((update_scan_kernel<DT, VEC, NI, U, ONE_>), grid,        \
+                     dim3(SCAN_T), 0, s, static_cast<const T*>(x), ids,       \
+                     w.part, w.bpart, (int)N, (int)K, (int)D, (int)w.nunits,  \
+                     (int)w.nblocks, choose_ur(B, N), kpw, vec4, fa, ctrl)
+  const bool one = FKC_SCAN_ONE && kpw == 1;
+  if (N <= 8 * SCAN_T) {
+    if (one)
+      FKC_SCAN_LAUNCH(2, true);
+    else
+      FKC_SCAN_LAUNCH(2, false);
+  } else {
+    if (one)
+      FKC_SCAN_LAUNCH(SCAN_UMAX, true);
+    else
+      FKC_SCAN_LAUNCH(SCAN_UMAX, false);
+  }
+#undef FKC_SCAN_LAUNCH
   return check_launch("update_scan");
 }
 
