@@ -969,21 +969,22 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
   for (int u = 0; u < SCAN_U; ++u)
 #pragma unroll
     for (int c = 0; c < 4; ++c) below += (unsigned)lab[u][c] < (unsigned)k0 ? 1 : 0;
-  below = wave_sum_i(below);
+  below = __builtin_amdgcn_readlane(wave_incl_scan(below), 63);
   if (lane == 0) s_red[wave] = below;
   // ONE: chunk (u, wave) holds points 4 (SCAN_T u + 64 wave) .. + 255, so
   // chunk q = SCAN_W u + wave runs in index order; rk[u] is this lane's
   // first match's rank inside its chunk (the matches of lower lanes).  The
   // lanes' match counts of three quads share a word (10-bit fields: a
   // chunk holds at most 256), so one DPP scan ranks three chunks.
-  // own: bit 4u + c set when label (u, c) is the owned one.
+  // own: bit 4u + c set when label (u, c) is the owned one (built from the
+  // last slot down, one shift-and-add per label).
   int rk[ONE ? SCAN_U : 1];
   uint32_t own = 0u;
   if constexpr (ONE) {
 #pragma unroll
-    for (int u = 0; u < SCAN_U; ++u)
+    for (int u = SCAN_U - 1; u >= 0; --u)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) own |= (lab[u][c] == k0 ? 1u : 0u) << (4 * u + c);
+      for (int c = 3; c >= 0; --c) own = own + own + (lab[u][c] == k0 ? 1u : 0u);
     constexpr int NW = (SCAN_U + 2) / 3;
     int pk[NW];
 #pragma unroll
