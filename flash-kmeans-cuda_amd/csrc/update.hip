@@ -892,14 +892,18 @@ constexpr int SCAN_BM = SCAN_KPW * SCAN_NMAX / 32;   // bitmap words (64 KB)
 
 // SCAN_U: label quads per thread (N <= 4 * SCAN_T * SCAN_U).  ONE: the
 // workgroup owns one label (kpw == 1).  Its rows are then placed without
-// bitmaps: for each 256-point chunk (one wave's labels of one quad index u)
-// the wave takes a ballot per quad slot, the chunks' match counts are
-// scanned once in chunk order (which is index order), and a row's sorted
-// position is its chunk's offset plus the matches in lower lanes (mbcnt)
-// and in its own lane's lower slots.  The bitmap's LDS then holds the
-// run's unit partials when they fit (a run over a few units), so the merge
-// reads them from LDS instead of the workspace.  Positions, pieces and
-// summation order are those of the bitmap path, so the bits are the same.
+// bitmaps: each lane keeps a mask of its owned slots and the owned counts
+// of its quads, packed three to a word, so a few DPP scans rank every
+// 256-point chunk (one wave's labels of one quad index u); the chunk totals
+// are scanned once in chunk order (which is index order), and each lane
+// loops over its own set bits only: a row's sorted position is its chunk's
+// offset plus the owned rows of lower lanes and of its own lower slots.
+// The bitmap's LDS then holds the run's unit partials when they fit (a run
+// over a few units), which wave 0 merges straight into the finalize.  The
+// kernel issues the same instructions on 16 waves per CU, so it is bound by
+// their count: this form avoids the bitmap walk's per-word loops and
+// branches.  Positions, pieces and summation order are those of the bitmap
+// path, so the bits are the same.
 template <int DT, int VEC, int NI, int SCAN_U, bool ONE>
 __global__ void __launch_bounds__(SCAN_T)
 update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
