@@ -7,6 +7,7 @@ library is loaded after torch so that both share torch's HIP runtime
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
@@ -92,9 +93,23 @@ def dtype_code(dt: torch.dtype) -> int:
         raise RuntimeError(f"unsupported dtype {dt}") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
-    """hipStream_t of torch's current stream on t's device."""
+    """hipStream_t of torch's current stream on t's device (the raw query
+    costs ~0.1 us against ~2 us for building the Stream object)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def on_device(t: torch.Tensor):
+    """Context making t's device current; a no-op context when it already
+    is (entering torch.cuda.device costs ~1.4 us per call)."""
+    if t.device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(t.device)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -105,7 +105,7 @@ def batch_kmeans_Euclid(
             cur, nxt = nxt, cur
         return cluster_ids, cur, n_iters_run
 
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         dt = _lib.dtype_code(x.dtype)
         ws = _lib.workspace(
             _lib.lib.fkc_kmeans_workspace_bytes(B, N, K, D, dt, max(max_iters, 1)),
