@@ -121,6 +121,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #ifndef FKC_X_NT
 #define FKC_X_NT 0
 #endif
+// FKC_WHOLE_STAGE=0 (compile time, for A/B builds) keeps small exact-index
+// tables on the double-buffered 64-row stages.
+#ifndef FKC_WHOLE_STAGE
+#define FKC_WHOLE_STAGE 1
+#endif
 
 constexpr int KC = 64;  // centroid rows per register-staged LDS stage
 constexpr int THREADS = 256;  // 4 waves
@@ -224,9 +229,13 @@ __device__ inline void progress_prio(int done, int total) {
 // flag: the unpadded variants carry no per-load condition); EXACT: track
 // the exact index in the loop instead of re-scoring at the end; SAVE: keep
 // the best block's scores (fold_saved) instead of re-scoring at the end
-// (two waves per SIMD, 128-row stages).  D % 8 == 0 so every 8-feature
-// segment is a 16-byte load.
-template <int DT, int DS2, int PT, bool PAD, bool EXACT, bool SAVE>
+// (two waves per SIMD, 128-row stages); WHOLE (exact index, direct stages):
+// the table in one single-buffered stage of up to 256 rows (64 KB at
+// D = 128), loaded in one round trip with one barrier, where the
+// double-buffered 64-row stages take one round trip each.  D % 8 == 0 so
+// every 8-feature segment is a 16-byte load.
+template <int DT, int DS2, int PT, bool PAD, bool EXACT, bool SAVE,
+          bool WHOLE = false>
 __global__ void __launch_bounds__(THREADS,
                                   PT == 8 ? 2
                                   : (SAVE && DS2 == 2) ? 3
@@ -336,7 +345,8 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // the same 16 KB per stage with more rows (D = 32: 256 rows, 0.026 ->
     // 0.021 ms at (2, 30000, 2000, 32); D = 64: 128 rows, ~1%), so a stage
     // still spans enough matrix work to hide its barrier.
-    constexpr int KCD0 = PT == 8    ? FKC_KC_DMA8
+    constexpr int KCD0 = WHOLE      ? (DS2 <= 4 ? 256 : 128)
+                         : PT == 8    ? FKC_KC_DMA8
                          : SAVE     ? FKC_KC_DMA_SAVE
                          : DS2 == 1 ? 4 * FKC_KC_DMA
                          : DS2 == 2 ? 2 * FKC_KC_DMA
@@ -351,9 +361,9 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     static_assert(STAGE % (THREADS * 16) == 0 && QW <= 64, "stage split");
     static_assert((ROWB & (ROWB - 1)) == 0, "power-of-two stage rows");
     __shared__ __attribute__((aligned(1024))) uint8_t s_c0[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t s_c1[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_c1[WHOLE ? 16 : STAGE];
     __shared__ __attribute__((aligned(256))) float s_q0[KCD];
-    __shared__ __attribute__((aligned(256))) float s_q1[KCD];
+    __shared__ __attribute__((aligned(256))) float s_q1[WHOLE ? 4 : KCD];
     typedef __attribute__((address_space(3))) void lvoid;
 
     const int uwave = __builtin_amdgcn_readfirstlane(wave);  // scalar copy
@@ -521,6 +531,18 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
     // The wait for the next stage's loads stays at the end of the stage:
     // the scheduling barrier keeps the compiler from hoisting it above the
     // stage's matrix work.
+    if constexpr (WHOLE) {
+      // One buffer (the plan takes this variant where the table is one
+      // stage; more stages run one after the other).
+      for (int chunk = 0; chunk < nch; ++chunk) {
+        if (chunk > 0) __syncthreads();  // the previous stage is read
+        issue(chunk, s_c0, s_q0);
+        __builtin_amdgcn_s_waitcnt(0);
+        fixq(chunk, s_q0);
+        __syncthreads();
+        compute(chunk, s_c0, s_q0);
+      }
+    } else {
     issue(0, s_c0, s_q0);
     __builtin_amdgcn_s_waitcnt(0);
     fixq(0, s_q0);
@@ -540,6 +562,7 @@ assign_mfma_kernel(const uint16_t* __restrict__ x,
       __builtin_amdgcn_s_waitcnt(0);
       fixq(chunk + 2, s_q0);
       __syncthreads();
+    }
     }
   } else {
     // Stages through VGPRs into padded LDS rows (row stride DP + 8 halves).
@@ -1100,7 +1123,8 @@ struct Slices {
 // ev0 / ev1 (both null or both set): events that the dispatch packets
 // themselves stamp, ev0 at the start of the scoring kernel and ev1 at the
 // end of the last kernel (no marker packets in the stream).
-template <int DT, int DS2, int PT, bool PAD, bool EXACT, bool SAVE>
+template <int DT, int DS2, int PT, bool PAD, bool EXACT, bool SAVE,
+          bool WHOLE = false>
 int launch_mfma_t(const void* x, const void* c, const float* c_sq,
                   int32_t* ids, int64_t B, int64_t N, int64_t K, int64_t D,
                   const int32_t* ctrl, const Slices& sl, hipStream_t s,
@@ -1111,13 +1135,13 @@ int launch_mfma_t(const void* x, const void* c, const float* c_sq,
             (unsigned)sl.S);
   const int kspan = merge ? sl.kspan : (int)K;
   if (ev0 != nullptr)
-    hipExtLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT, SAVE>), grid,
+    hipExtLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT, SAVE, WHOLE>), grid,
                           dim3(THREADS), 0, s, ev0, merge ? nullptr : ev1, 0,
                           static_cast<const uint16_t*>(x),
                           static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
                           (int)K, (int)D, ctrl, kspan, sl.psc, sl.pidx);
   else
-    hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT, SAVE>), grid,
+    hipLaunchKernelGGL((assign_mfma_kernel<DT, DS2, PT, PAD, EXACT, SAVE, WHOLE>), grid,
                        dim3(THREADS), 0, s, static_cast<const uint16_t*>(x),
                        static_cast<const uint16_t*>(c), c_sq, ids, (int)N,
                        (int)K, (int)D, ctrl, kspan, sl.psc, sl.pidx);
@@ -1139,7 +1163,7 @@ using MfmaLauncher = int (*)(const void*, const void*, const float*, int32_t*,
                              hipEvent_t, hipEvent_t);
 
 template <int DT, int DS2, int PT>
-constexpr MfmaLauncher entry(bool pad, bool exact, bool save) {
+constexpr MfmaLauncher entry(bool pad, bool exact, bool save, bool whole) {
   if constexpr (PT == 8) {
     // Direct stages and the re-score epilogue only (DS2 = 4, unpadded).
     if constexpr (DS2 == 4) {
@@ -1155,6 +1179,11 @@ constexpr MfmaLauncher entry(bool pad, bool exact, bool save) {
       }
       return nullptr;
     }
+    if constexpr (DS2 == 1 || DS2 == 2 || DS2 == 4 || DS2 == 8) {
+      // One whole-table stage: exact index, unpadded, direct stages.
+      if (whole && exact && !pad)
+        return &launch_mfma_t<DT, DS2, PT, false, true, false, true>;
+    }
     if (exact)
       return pad ? &launch_mfma_t<DT, DS2, PT, true, true, false>
                  : &launch_mfma_t<DT, DS2, PT, false, true, false>;
@@ -1169,35 +1198,36 @@ constexpr MfmaLauncher entry(bool pad, bool exact, bool save) {
 // re-score epilogue).  The 1/2/4 variants keep the point registers
 // (PT * DS2 * 4 VGPRs) at <= 64; the eight-tile one holds 128.
 template <int DT, int DS2>
-MfmaLauncher by_pt(int pt, bool pad, bool exact, bool save) {
+MfmaLauncher by_pt(int pt, bool pad, bool exact, bool save, bool whole) {
   switch (pt) {
-    case 1: return entry<DT, DS2, 1>(pad, exact, save);
-    case 2: return entry<DT, DS2, 2>(pad, exact, save);
-    case 4: return entry<DT, DS2, 4>(pad, exact, save);
-    case 8: return entry<DT, DS2, 8>(pad, exact, save);
+    case 1: return entry<DT, DS2, 1>(pad, exact, save, whole);
+    case 2: return entry<DT, DS2, 2>(pad, exact, save, whole);
+    case 4: return entry<DT, DS2, 4>(pad, exact, save, whole);
+    case 8: return entry<DT, DS2, 8>(pad, exact, save, whole);
     default: return nullptr;
   }
 }
 
 template <int DT>
-MfmaLauncher mfma_launcher(int ds2, int pt, bool pad, bool exact, bool save) {
+MfmaLauncher mfma_launcher(int ds2, int pt, bool pad, bool exact, bool save,
+                           bool whole) {
   switch (ds2) {
-    case 1: return by_pt<DT, 1>(pt, pad, exact, save);
-    case 2: return by_pt<DT, 2>(pt, pad, exact, save);
-    case 3: return by_pt<DT, 3>(pt, pad, exact, save);
-    case 4: return by_pt<DT, 4>(pt, pad, exact, save);
-    case 5: return by_pt<DT, 5>(pt, pad, exact, save);
-    case 6: return by_pt<DT, 6>(pt, pad, exact, save);
-    case 7: return by_pt<DT, 7>(pt, pad, exact, save);
-    case 8: return by_pt<DT, 8>(pt, pad, exact, save);
-    case 9: return by_pt<DT, 9>(pt, pad, exact, save);
-    case 10: return by_pt<DT, 10>(pt, pad, exact, save);
-    case 11: return by_pt<DT, 11>(pt, pad, exact, save);
-    case 12: return by_pt<DT, 12>(pt, pad, exact, save);
-    case 13: return by_pt<DT, 13>(pt, pad, exact, save);
-    case 14: return by_pt<DT, 14>(pt, pad, exact, save);
-    case 15: return by_pt<DT, 15>(pt, pad, exact, save);
-    case 16: return by_pt<DT, 16>(pt, pad, exact, save);
+    case 1: return by_pt<DT, 1>(pt, pad, exact, save, whole);
+    case 2: return by_pt<DT, 2>(pt, pad, exact, save, whole);
+    case 3: return by_pt<DT, 3>(pt, pad, exact, save, whole);
+    case 4: return by_pt<DT, 4>(pt, pad, exact, save, whole);
+    case 5: return by_pt<DT, 5>(pt, pad, exact, save, whole);
+    case 6: return by_pt<DT, 6>(pt, pad, exact, save, whole);
+    case 7: return by_pt<DT, 7>(pt, pad, exact, save, whole);
+    case 8: return by_pt<DT, 8>(pt, pad, exact, save, whole);
+    case 9: return by_pt<DT, 9>(pt, pad, exact, save, whole);
+    case 10: return by_pt<DT, 10>(pt, pad, exact, save, whole);
+    case 11: return by_pt<DT, 11>(pt, pad, exact, save, whole);
+    case 12: return by_pt<DT, 12>(pt, pad, exact, save, whole);
+    case 13: return by_pt<DT, 13>(pt, pad, exact, save, whole);
+    case 14: return by_pt<DT, 14>(pt, pad, exact, save, whole);
+    case 15: return by_pt<DT, 15>(pt, pad, exact, save, whole);
+    case 16: return by_pt<DT, 16>(pt, pad, exact, save, whole);
     default: return nullptr;
   }
 }
@@ -1258,6 +1288,7 @@ static int choose_pt(int ds2, bool pad, bool exact, int64_t B, int64_t N,
 struct Plan {
   int ds2, pt, S, kspan;
   bool pad, exact, save;
+  bool whole = false;  // exact index, the table in one direct stage
   bool resident = false;  // assign_resident_kernel (pt: its tiles per wave)
 };
 
@@ -1356,6 +1387,14 @@ static Plan plan_assign(int64_t B, int64_t N, int64_t K, int64_t D,
     return p;
   }
   p.save = use_save(p, grid_wgs(p.pt, B, N));
+  // One whole-table stage (64 KB at D = 128) where the table fits it and
+  // the grid is one round of two workgroups per CU (the stage's LDS allows
+  // two): one load round trip and one barrier instead of one per 64-row
+  // stage.
+  p.whole = FKC_WHOLE_STAGE && FKC_USE_DMA && p.exact && !p.pad &&
+            (p.ds2 == 1 || p.ds2 == 2 || p.ds2 == 4 || p.ds2 == 8) &&
+            K <= (p.ds2 <= 4 ? 256 : 128) &&
+            grid_wgs(p.pt, B, N) <= 2 * device_shape().cus;
   if (!can_slice || p.exact) return p;
   // Four tiles, not eight: on sliced-size grids four tiles on ~256
   // workgroups beat eight on 512 (N = 8192, K = 65536: 0.150 vs 0.166 ms;
@@ -1457,8 +1496,8 @@ int launch_assign_mfma(const void* x, const void* c, const float* c_sq,
                 ws_bytes, need);
   MfmaLauncher fn =
       dtype == FKC_F16
-          ? mfma_launcher<FKC_F16>(p.ds2, p.pt, p.pad, p.exact, p.save)
-          : mfma_launcher<FKC_BF16>(p.ds2, p.pt, p.pad, p.exact, p.save);
+          ? mfma_launcher<FKC_F16>(p.ds2, p.pt, p.pad, p.exact, p.save, p.whole)
+          : mfma_launcher<FKC_BF16>(p.ds2, p.pt, p.pad, p.exact, p.save, p.whole);
   if (!fn)
     return fail(FKC_ERR_UNSUPPORTED, "assign: no MFMA variant for D=%lld",
                 (long long)D);
