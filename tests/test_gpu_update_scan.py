@@ -9,7 +9,8 @@ read one by one instead of four at a time), odd and wide feature widths
 labels per workgroup, empty clusters, one point, tol > 0, and rows whose
 points crowd into a few labels: runs over many units, whole 64-unit blocks
 summed as block partials, and a label with more rows than one placement
-window holds.
+window holds; and, for one label per workgroup, runs sized on both sides
+of the LDS room for unit partials.
 """
 
 from __future__ import annotations
@@ -108,3 +109,37 @@ def test_scan_update_with_tol(monkeypatch):
     a, b = _both(monkeypatch, xt, cfg.K, it, 30, tol=1e-3)
     _same(a, b, "tol")
     assert a[2] < 30
+
+
+@pytest.mark.parametrize("D,dtype", [(512, "f16"), (256, "bf16")])
+def test_scan_update_lds_partial_boundary(monkeypatch, D, dtype):
+    """One label per workgroup: a run over several units keeps its unit
+    partials in LDS only while (units spanned) x D fits the 16384-float
+    region (32 units of 32 rows at D = 512, 64 at D = 256) and no whole
+    64-unit block lies inside it.  Labels sized around that capacity (and a
+    few long enough for whole blocks) must give the sort path's bits either
+    way.  Points are copies of well separated centroids plus small noise, so
+    the label sizes are set by construction."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    print(f"D={D} {dtype}", flush=True)
+    rng = np.random.default_rng(D)
+    cap_rows = 16384 // D * 32
+    sizes = [cap_rows - 64 + 16 * i for i in range(9)]   # both sides of the capacity
+    sizes += [2100, 2600, 3100]                          # whole 64-unit blocks inside
+    sizes += [37, 5, 1, 90, 300]
+    K = len(sizes) + 3                                   # three empty labels
+    cent = rng.standard_normal((K, D)).astype(np.float32) * 8
+    rows = [cent[k] + rng.standard_normal((n, D)).astype(np.float32) * 0.01
+            for k, n in enumerate(sizes)]
+    x = np.concatenate(rows)[rng.permutation(sum(sizes))]
+    assert x.shape[0] <= 32768
+    x = O.from_f32(x[None], dtype)
+    init = O.from_f32(cent[None], dtype)
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a, b = _both(monkeypatch, xt, K, it, 3)
+    _same(a, b, "scan vs sort")
+    c = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it, verbose=True)
+    _same(a, c, "loop vs per-op path")
+    counts = np.bincount(a[0].cpu().numpy()[0], minlength=K)
+    assert counts[:len(sizes)].tolist() == sizes and counts[len(sizes):].sum() == 0
+
