@@ -441,6 +441,36 @@ def test_loop_with_sliced_assign(monkeypatch, B, N, K, dtype):
         assert torch.equal(a[0], r[0]) and torch.equal(a[1], r[1])
 
 
+@pytest.mark.parametrize("B,N,K,D,dtype,ksplit,save,tol", [
+    (1, 16384, 8192, 128, "f16", None, None, 0.0),  # the plan's own slices (kept scores)
+    (1, 12000, 6000, 128, "bf16", "3", "0", 0.0),   # re-score epilogue, three slices
+    (2, 5000, 4500, 128, "f16", "2", "1", 0.0),     # batches, kept scores
+    (1, 9000, 5000, 64, "bf16", "4", None, 0.0),    # D = 64, four slices
+    (1, 7000, 4097, 128, "f16", "3", None, 1e-3),   # tol stop: later launches exit at once
+])
+def test_loop_with_sliced_assign_variants(monkeypatch, B, N, K, D, dtype,
+                                          ksplit, save, tol):
+    """Sliced assigns inside the Lloyd loop (its workspace holding the
+    partial winners) across slice counts, both epilogues (kept scores and
+    re-score), batches, D = 64 and a tol stop: the loop and the per-op path
+    give the same labels, centroids and iteration count."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    for k, v in (("FKC_KSPLIT", ksplit), ("FKC_SAVE", save)):
+        if v is None:
+            monkeypatch.delenv(k, raising=False)
+        else:
+            monkeypatch.setenv(k, v)
+    print(f"B={B} N={N} K={K} D={D} {dtype} ksplit={ksplit} save={save} tol={tol}", flush=True)
+    rng = np.random.default_rng(N + K)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32), dtype)
+    init = np.ascontiguousarray(x[:, :K])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    a = batch_kmeans_Euclid(xt, K, max_iters=6, tol=tol, init_centroids=it)
+    b = batch_kmeans_Euclid(xt, K, max_iters=6, tol=tol, init_centroids=it, verbose=True)
+    assert a[2] == b[2]
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 @pytest.mark.parametrize("B,N,K,D,dtype,tol", [
     (8, 65536, 1024, 64, "bf16", 0.0),    # c4's shape: resident by default
     (2, 40000, 700, 64, "bf16", 1e-4),    # forced resident, tol stop
