@@ -942,10 +942,9 @@ update_scan_kernel(const typename Elem<DT>::T* __restrict__ x,
 
   // 1. The row's labels stay in registers: thread t holds labels
   // 4 (t + SCAN_T u) + c, u < SCAN_U, c < 4.  All loads are in flight
-  // before any is used; -1 past N.
-  // Branch-free: indices are clamped into the row and labels past N read
-  // as INT_MAX (never owned, never below k0).  vec4 implies N % 4 == 0, so
-  // a quad is wholly inside the row or wholly past it.
+  // before any is used.  Branch-free: indices are clamped into the row and
+  // labels past N read as INT_MAX (never owned, never below k0).  vec4
+  // implies N % 4 == 0, so a quad is wholly inside the row or wholly past it.
   int lab[SCAN_U][4];
   if (vec4) {
 #pragma unroll
