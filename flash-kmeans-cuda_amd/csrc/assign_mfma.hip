@@ -813,7 +813,8 @@ assign_merge_kernel(const float* __restrict__ psc,
 // ------------------------------------------------------------------------
 // Centroid-resident variant.  When a batch row's whole centroid table fits
 // in one workgroup's LDS (Kp = K rounded up to 32 rows of DP features, plus
-// Kp scaled c_sq values: resident_bytes(Kp) <= the device's LDS per
+// Kp scaled c_sq values and a little padding: resident_bytes(Kp) <= the
+// device's LDS per
 // workgroup, i.e. on gfx950's 160 KiB K <= 1216 at D = 64 and K <= 2400 at
 // D = 32), each workgroup loads the table once
 // and its waves then walk their 16*PT-point tiles against it on their own:
@@ -827,8 +828,14 @@ assign_merge_kernel(const float* __restrict__ psc,
 // gfx950, read with the CU count by device_shape()).
 constexpr int kResidentWaves = 16;        // waves per workgroup (4 per SIMD)
 
+// The table, its scaled c_sq, and room for the loop's fragment read one
+// block past the table (rows Kp .. Kp + 15 and c_sq entries Kp .. Kp + 15,
+// read in the last trip and never used): the rows fall on the c_sq region
+// and past it by 16 rows' bytes less that region, the c_sq entries 64 bytes
+// past it.
 __host__ __device__ constexpr int resident_bytes(int ds2, int Kp) {
-  return Kp * (ds2 * 64 + 4);
+  return Kp * (ds2 * 64 + 4) +
+         (16 * ds2 * 64 > 4 * Kp ? 16 * ds2 * 64 - 4 * Kp : 0) + 64;
 }
 
 // W waves per workgroup, PT tiles per wave: 16 x 8 at D = 32 (a block's
@@ -946,7 +953,11 @@ assign_resident_kernel(const uint16_t* __restrict__ x,
     // MFMAs run while block t+1's fragments are read and block t-1 is
     // folded; the table has an even number of blocks (Kp % 32 == 0).  The
     // fold of the -inf seed before block 0 changes nothing, and the read
-    // past the last block re-reads block 0.  Eight tiles have no registers
+    // past the last block lands in the table's padding (resident_bytes) and
+    // is never used: unclamped, the third read of a trip is the first one's
+    // address plus a constant, so it costs no address arithmetic (measured
+    // 1.5-2.5% faster at D = 32 and 64 than wrapping to block 0, the same
+    // labels).  Eight tiles have no registers
     // for a second accumulator set: each block is folded after its own
     // MFMAs (the other waves of the SIMD cover the wait).
     u32x4 a0[DS2], a1[DS2];
@@ -987,7 +998,7 @@ assign_resident_kernel(const uint16_t* __restrict__ x,
       else
         fold(accB, 16 * (t - 1));
       hint();
-      frag(t + 2 < nblk ? t + 2 : 0, a0, c0);
+      frag(t + 2, a0, c0);
       chain(a1, c1, accB);
       if constexpr (PT >= 8)
         fold(accB, 16 * (t + 1));
@@ -1342,7 +1353,8 @@ static bool use_resident(const Plan& p, int64_t B, int64_t N, int64_t K) {
   if (p.pad || (p.ds2 != 1 && p.ds2 != 2)) return false;
   const int64_t Kp = (K + 31) & ~int64_t{31};
   const DeviceShape dev = device_shape();
-  if (Kp * (p.ds2 * 64 + 4) > dev.lds_per_wg) return false;
+  if (Kp > 65536 || resident_bytes(p.ds2, (int)Kp) > dev.lds_per_wg)
+    return false;
   const int o = resident_override();
   if (o >= 0) return o == 1;
   const int pt = resident_pt(p.ds2);
