@@ -10,7 +10,8 @@ labels per workgroup, empty clusters, one point, tol > 0, and rows whose
 points crowd into a few labels: runs over many units, whole 64-unit blocks
 summed as block partials, and a label with more rows than one placement
 window holds; and, for one label per workgroup, runs sized on both sides
-of the LDS room for unit partials.
+of the LDS room for unit partials.  The two switches that reshape the
+update (labels per workgroup, rows per unit) are swept too.
 """
 
 from __future__ import annotations
@@ -143,3 +144,71 @@ def test_scan_update_lds_partial_boundary(monkeypatch, D, dtype):
     counts = np.bincount(a[0].cpu().numpy()[0], minlength=K)
     assert counts[:len(sizes)].tolist() == sizes and counts[len(sizes):].sum() == 0
 
+
+
+@pytest.mark.parametrize("B,N,K,D,dtype", [
+    (2, 20000, 300, 64, "bf16"),
+    (1, 32768, 256, 128, "f16"),     # c2
+])
+def test_scan_update_labels_per_workgroup(monkeypatch, B, N, K, D, dtype):
+    """FKC_SCAN_WGS sets how many workgroups share a row's labels (labels per
+    workgroup kpw = ceil(B K / FKC_SCAN_WGS)): one label each (the one-label
+    form), a few, the most the bitmap form holds (16), and one more than
+    that (17: the plan then takes the sort path).  Positions, units and
+    summation order do not depend on kpw, so every setting gives the sort
+    path's bits."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    print(f"B={B} N={N} K={K} D={D} {dtype}", flush=True)
+    rng = np.random.default_rng(B * N + K)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32) * 2, dtype)
+    init = np.ascontiguousarray(x[:, rng.choice(N, K, replace=False)])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    monkeypatch.setenv("FKC_UPDATE_SCAN", "0")
+    ref = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it)
+    monkeypatch.setenv("FKC_UPDATE_SCAN", "1")
+    BK = B * K
+    for kpw in [1, 2, 3, 7, 16, 17]:
+        monkeypatch.setenv("FKC_SCAN_WGS", str(-(-BK // kpw)))
+        got = batch_kmeans_Euclid(xt, K, max_iters=3, init_centroids=it)
+        _same(got, ref, f"kpw {kpw}")
+    monkeypatch.delenv("FKC_SCAN_WGS")
+    monkeypatch.delenv("FKC_UPDATE_SCAN")
+
+
+@pytest.mark.parametrize("B,N,K,D,dtype", [
+    (1, 20000, 200, 128, "bf16"),    # sort-free update
+    (2, 40000, 300, 64, "f16"),      # sort path
+])
+def test_update_rows_per_unit(monkeypatch, B, N, K, D, dtype):
+    """FKC_UPDATE_ROWS (32, 64 or 128 rows per unit) changes the summation
+    bracketing, so centroids may differ from the automatic choice by fp32
+    accumulation error (bounded here by 1e-4 absolute: ~200 rows of |x| < 10
+    at 2^-23 each, far looser than typical) plus one unit in the last place
+    of the storage type.  For each setting the sort-free update still equals
+    the sort path and the loop equals the per-op path bit for bit; the
+    one-iteration labels never change (they come from the initial
+    centroids)."""
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    print(f"B={B} N={N} K={K} D={D} {dtype}", flush=True)
+    rng = np.random.default_rng(N + K + D)
+    x = O.from_f32(rng.standard_normal((B, N, D)).astype(np.float32) * 2, dtype)
+    init = np.ascontiguousarray(x[:, rng.choice(N, K, replace=False)])
+    xt, it = _T(x, dtype), _T(init, dtype)
+    base = batch_kmeans_Euclid(xt, K, max_iters=1, init_centroids=it)
+    c0 = O.to_f64(_np_of(base[1], dtype), dtype)
+    ulp = 2.0 ** (-10 if dtype == "f16" else -7)
+    for ur in ["32", "64", "128"]:
+        monkeypatch.setenv("FKC_UPDATE_ROWS", ur)
+        a, b = _both(monkeypatch, xt, K, it, 1)
+        _same(a, b, f"rows {ur}: scan vs sort")
+        c = batch_kmeans_Euclid(xt, K, max_iters=1, init_centroids=it, verbose=True)
+        _same(a, c, f"rows {ur}: loop vs per-op path")
+        assert torch.equal(a[0], base[0]), ur
+        cu = O.to_f64(_np_of(a[1], dtype), dtype)
+        assert np.all(np.abs(cu - c0) <= ulp * np.abs(c0) + 1e-4), ur
+    monkeypatch.delenv("FKC_UPDATE_ROWS")
+
+
+def _np_of(t, dtype):
+    from flash_kmeans_cuda import synth
+    return synth.from_torch(t, dtype)
