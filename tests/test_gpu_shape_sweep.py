@@ -16,6 +16,7 @@ Each case checks:
 
 The near-tie bar is the assign tests' 2^-16 of ||x||^2 + ||c||^2, widened in
 proportion for D > 256 (the fp32 dot product's error bound grows with D).
+A fixed list of edge shapes runs the same checks.
 """
 
 from __future__ import annotations
@@ -116,6 +117,37 @@ def test_small_shapes(monkeypatch, case):
 
 @pytest.mark.parametrize("case", LARGE, ids=_case_id)
 def test_large_shapes(case):
+    from flash_kmeans_cuda import batch_kmeans_Euclid
+    B, N, K, D, dt, crowd, seed = case
+    print(_case_id(case), flush=True)
+    xs, _, xt, it, rng = _inputs(*case)
+    a = batch_kmeans_Euclid(xt, K, max_iters=2, init_centroids=it)
+    c = batch_kmeans_Euclid(xt, K, max_iters=2, init_centroids=it, verbose=True)
+    _same(a, c, "loop vs per-op path")
+    _check_labels(xs, xt, it, K, D, dt, a[0].cpu().numpy(), 2, rng)
+
+
+EDGE = [
+    (1, 1000, 100000, 16, "f16", False, 1),    # K far above N
+    (64, 1000, 10, 8, "bf16", False, 2),       # many batch rows
+    (1, 4096, 64, 1024, "f16", False, 3),      # D above the matrix-core route
+    (1, 1 << 22, 16, 8, "f16", False, 4),      # 4M points, tiny K and D
+    (3, 70000, 4097, 200, "bf16", False, 5),   # padded width, K one past a power of two
+    (1, 100, 1, 4, "f32", False, 6),           # one cluster
+    (2, 33000, 65535, 8, "f16", False, 7),     # K = 2^16 - 1, N just past the sort-free rows
+    (1, 8192, 65536, 128, "bf16", False, 8),   # centroid slices
+    (5, 3, 7, 520, "f16", False, 9),           # three points per row, D past 512
+    (1, 50000, 300, 600, "f32", False, 10),    # wide fp32 rows
+    (128, 256, 256, 32, "bf16", False, 11),    # 128 short batch rows
+]
+
+
+@pytest.mark.parametrize("case", EDGE, ids=_case_id)
+def test_edge_shapes(case):
+    """Shapes at the edges of what the plans choose between: K far above N,
+    many rows, widths past the matrix-core route, millions of points, one
+    cluster, K near 2^16 with N just past the sort-free update's 32768 rows,
+    centroid slices."""
     from flash_kmeans_cuda import batch_kmeans_Euclid
     B, N, K, D, dt, crowd, seed = case
     print(_case_id(case), flush=True)
